@@ -1,0 +1,128 @@
+// Host side of exactsample_amd: launch geometry, dtype dispatch and the C ABI
+// (include/exactsample_amd.h).
+#include <limits.h>
+#include <stdio.h>
+#include "es_layout.h"
+#include "es_plan.h"
+
+namespace {
+constexpr int kBlock = 256;  // threads per block of the kernel
+thread_local char g_last_hip_error[256] = "";
+
+constexpr int64_t elem_size(int dt) { return dt == ES_F64 ? 8 : dt == ES_F32 ? 4 : 2; }
+
+// Rows contiguous and aligned to a group of four elements (target and draft).
+bool vectorizable_matrix(const es_arguments& a, const es_matrix& m) {
+  const int64_t es = elem_size(m.dtype);
+  return !m.data || (m.s1 == 1 && a.vocab % 4 == 0 && (m.s0 * es) % (4 * es) == 0 &&
+                     reinterpret_cast<uintptr_t>(m.data) % uintptr_t(4 * es) == 0);
+}
+template <int DT> bool vectorizable(const es_arguments& a) {
+  return vectorizable_matrix(a, a.target) && vectorizable_matrix(a, a.draft);
+}
+
+// Per-thread register tile (groups of four) and slices per row. Prefer the
+// largest tile that still gives enough blocks to fill 256 CUs.
+struct Geometry { int g, slices; };
+Geometry choose_geometry(int64_t rows, int64_t groups, bool large_tiles) {
+  const int large[] = {16, 8, 4};
+  const int small[] = {4, 4, 4};  // strided rows, f16 and f64 use the 4-group tile only
+  const int* options = large_tiles ? large : small;
+  Geometry best{options[0], int((groups + int64_t(options[0]) * kBlock - 1) / (int64_t(options[0]) * kBlock))};
+  for (int k = 0; k < 3; ++k) {
+    const int g = options[k];
+    const int64_t s = (groups + int64_t(g) * kBlock - 1) / (int64_t(g) * kBlock);
+    if (s > es::MAX_SLICES) break;
+    best = Geometry{g, int(s)};
+    if (rows * s >= 1024) break;
+  }
+  return best;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t es_workspace_size(int64_t rows, int64_t vocab, int32_t reference) {
+  if (rows < 0 || vocab < 0) return 0;
+  const unsigned __int128 scratch = reference ? (unsigned __int128)vocab * 20u : 0u;
+  const unsigned __int128 per = es::ROW_RESULT_BYTES + (scratch > es::ROW_SCRATCH ? scratch : es::ROW_SCRATCH);
+  const unsigned __int128 total = es::HEADER_BYTES + (unsigned __int128)rows * per;
+  if (total > (unsigned __int128)SIZE_MAX) return 0;
+  return size_t(total);
+}
+
+size_t es_fallback_counter_offset(void) { return 4; }
+
+const char* es_error_string(int32_t code) {
+  switch (code) {
+    case ES_SUCCESS: return "success";
+    case ES_ERR_NULL_ARGUMENT: return "a required pointer argument is null";
+    case ES_ERR_BAD_DIMENSION: return "rows, requests, vocab or max_draft out of the supported range";
+    case ES_ERR_BAD_OPTION: return "mode, dispatch or list_max out of range";
+    case ES_ERR_WORKSPACE_SIZE: return "workspace capacity exceeded";
+    case ES_ERR_WORKSPACE_ALIGN: return "workspace alignment must be 8 bytes";
+    case ES_ERR_BAD_DTYPE: return "unsupported logits dtype (draft logits must match the target dtype)";
+    case ES_ERR_LAUNCH: return "exactsample kernel launch failed";
+    default: return "unknown exactsample_amd error";
+  }
+}
+
+const char* es_last_hip_error(void) { return g_last_hip_error; }
+
+int32_t es_launch(const es_arguments* args, void* stream_ptr) {
+  if (!args) return ES_ERR_NULL_ARGUMENT;
+  const es_arguments& a = *args;
+  g_last_hip_error[0] = 0;
+  if (a.requests < 0 || a.rows < 0 || a.vocab <= 0 || a.vocab > INT32_MAX || a.rows > 65535 ||
+      a.requests > INT32_MAX || a.max_draft < 0 || a.max_draft >= INT32_MAX)
+    return ES_ERR_BAD_DIMENSION;
+  if (a.requests == 0 && a.rows != 0) return ES_ERR_BAD_DIMENSION;
+  if (a.mode < 0 || a.mode > 1 || a.dispatch < 0 || a.dispatch > 2 || a.list_max < 0 || a.list_max > 256)
+    return ES_ERR_BAD_OPTION;
+  if (a.requests == 0) return ES_SUCCESS;
+  if (!a.target.data && a.rows > 0) return ES_ERR_NULL_ARGUMENT;
+  if (!a.cu_rows.data || !a.top_k.data || !a.draft_kind.data || !a.seed.data || !a.stream.data ||
+      !a.temperature.data || !a.top_p.data || !a.min_p.data || (!a.draft_ids && a.max_draft > 0) ||
+      !a.tokens || !a.accepted ||
+      !a.status || !a.path || !a.workspace || (!a.position.data && a.rows > 0))
+    return ES_ERR_NULL_ARGUMENT;
+  if (a.target.dtype < ES_F32 || a.target.dtype > ES_BF16) return ES_ERR_BAD_DTYPE;
+  if (a.draft.data && a.draft.dtype != a.target.dtype) return ES_ERR_BAD_DTYPE;
+  const size_t need = es_workspace_size(a.rows, a.vocab, a.dispatch == 1);
+  if (need == 0 || a.workspace_bytes < need) return ES_ERR_WORKSPACE_SIZE;
+  if (reinterpret_cast<uintptr_t>(a.workspace) % 8 != 0) return ES_ERR_WORKSPACE_ALIGN;
+  if (a.dispatch == 1) return ES_ERR_BAD_OPTION;  // the on-device reference path is not built yet
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const int64_t groups = (a.vocab + 3) / 4;
+  const bool large_tiles = (a.target.dtype == ES_F32 || a.target.dtype == ES_BF16) &&
+                           vectorizable_matrix(a, a.target) && vectorizable_matrix(a, a.draft);
+  const Geometry geo = choose_geometry(a.rows, groups, large_tiles);
+  es::Plan pl{};
+  pl.groups = int(groups);
+  pl.req_blocks = int((a.requests + kBlock - 1) / kBlock);
+  if (geo.slices > es::MAX_SLICES || a.rows == 0) {
+    pl.slices = 1;
+    pl.gps = int(groups);
+  } else {
+    pl.slices = geo.slices;
+    pl.gps = int((groups + geo.slices - 1) / geo.slices);
+  }
+  const int cap_total = a.target.dtype == ES_F64 ? es::cand_capacity<double>() : es::cand_capacity<float>();
+  pl.cap_slice = cap_total / pl.slices;
+  hipError_t err = hipSuccess;
+  if (geo.slices > es::MAX_SLICES) return ES_ERR_BAD_DIMENSION;  // vocabularies above ~1M are not supported yet
+  switch (a.target.dtype) {
+    case ES_F32: err = es::launch_dtype<ES_F32>(a, pl, geo.g, vectorizable<ES_F32>(a), stream); break;
+    case ES_F64: err = es::launch_dtype<ES_F64>(a, pl, geo.g, vectorizable<ES_F64>(a), stream); break;
+    case ES_F16: err = es::launch_dtype<ES_F16>(a, pl, geo.g, vectorizable<ES_F16>(a), stream); break;
+    default: err = es::launch_dtype<ES_BF16>(a, pl, geo.g, vectorizable<ES_BF16>(a), stream); break;
+  }
+  if (err != hipSuccess) {
+    snprintf(g_last_hip_error, sizeof(g_last_hip_error), "%s", hipGetErrorString(err));
+    return ES_ERR_LAUNCH;
+  }
+  return ES_SUCCESS;
+}
+
+}  // extern "C"

@@ -1,0 +1,191 @@
+// Device primitives for the gfx950 sampling path: 64-lane wave reductions,
+// block reductions in a fixed order, Philox4x32-10, order-preserving keys,
+// double-double sums and the FP32 Gumbel noise with its certified bound.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <math.h>
+#include "exactsample_amd.h"
+
+namespace es {
+
+constexpr int WAVE = 64;
+constexpr int BLOCK = 256;            // every kernel runs 4 waves of 64 lanes
+constexpr int WAVES = BLOCK / WAVE;
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (WAVE - 1); }
+__device__ __forceinline__ int wave_id() { return threadIdx.x / WAVE; }
+
+// ---------------------------------------------------------------------------
+// Cross-lane exchange. __shfl_xor over the full 64-lane wave.
+__device__ __forceinline__ float xshfl(float v, int m) { return __shfl_xor(v, m, WAVE); }
+__device__ __forceinline__ double xshfl(double v, int m) { return __shfl_xor(v, m, WAVE); }
+__device__ __forceinline__ int xshfl(int v, int m) { return __shfl_xor(v, m, WAVE); }
+__device__ __forceinline__ unsigned xshfl(unsigned v, int m) { return __shfl_xor(v, m, WAVE); }
+__device__ __forceinline__ uint64_t xshfl(uint64_t v, int m) {
+  return (uint64_t(__shfl_xor(unsigned(v >> 32), m, WAVE)) << 32) | __shfl_xor(unsigned(v), m, WAVE);
+}
+
+// op over all 64 lanes; every lane receives bitwise the same value because
+// each butterfly step combines the same two operands on both partners.
+template <class T, class Op> __device__ __forceinline__ T wave_all(T v, Op op) {
+#pragma unroll
+  for (int m = WAVE / 2; m; m >>= 1) v = op(v, xshfl(v, m));
+  return v;
+}
+
+// op over the block, combined across waves in wave order; every thread gets it.
+// `scratch` holds WAVES entries and may be reused right after the call.
+template <class T, class Op> __device__ __forceinline__ T block_all(T v, Op op, T* scratch) {
+  v = wave_all(v, op);
+  __syncthreads();
+  if (lane_id() == 0) scratch[wave_id()] = v;
+  __syncthreads();
+  T r = scratch[0];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) r = op(r, scratch[w]);
+  return r;
+}
+
+// Inclusive prefix sum over the wave in lane order.
+template <class T> __device__ __forceinline__ T wave_scan_add(T v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int o = 1; o < WAVE; o <<= 1) {
+    T y = __shfl_up(v, o, WAVE);
+    if (l >= o) v += y;
+  }
+  return v;
+}
+
+// Inclusive prefix sum over the block in thread order; *total receives the sum.
+__device__ __forceinline__ int block_scan_add(int v, int* scratch, int* total) {
+  int incl = wave_scan_add(v);
+  __syncthreads();
+  if (lane_id() == WAVE - 1) scratch[wave_id()] = incl;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) {
+    const int s = scratch[w];
+    before += w < wave_id() ? s : 0;
+    all += s;
+  }
+  *total = all;
+  return incl + before;
+}
+
+// ---------------------------------------------------------------------------
+// Philox4x32-10 (Random123), counter = (stream, position, substream, token/4),
+// key = (seed lo, seed hi). Contract: docs/rng.md:1-28 of the reference.
+struct Words { uint32_t w[4]; };
+
+__host__ __device__ __forceinline__ Words philox(uint64_t seed, uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3) {
+  uint32_t k0 = uint32_t(seed), k1 = uint32_t(seed >> 32);
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint64_t p0 = uint64_t(0xD2511F53u) * c0;
+    const uint64_t p1 = uint64_t(0xCD9E8D57u) * c2;
+    const uint32_t n0 = uint32_t(p1 >> 32) ^ c1 ^ k0;
+    const uint32_t n2 = uint32_t(p0 >> 32) ^ c3 ^ k1;
+    c1 = uint32_t(p1);
+    c3 = uint32_t(p0);
+    c0 = n0;
+    c2 = n2;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return Words{{c0, c1, c2, c3}};
+}
+
+struct RngAddr { uint64_t seed; uint32_t stream, position; };
+
+__device__ __forceinline__ uint32_t word_of(const RngAddr& r, uint32_t sub, uint32_t token) {
+  const Words w = philox(r.seed, r.stream, r.position, sub, token >> 2);
+  const uint32_t lane = token & 3u;
+  return lane == 0 ? w.w[0] : lane == 1 ? w.w[1] : lane == 2 ? w.w[2] : w.w[3];
+}
+
+// u = (w + 0.5) / 2^32, exact in FP64 (docs/rng.md:17-19).
+__host__ __device__ __forceinline__ double uniform64(uint32_t w) { return (double(w) + 0.5) * (1.0 / 4294967296.0); }
+
+// The oracle's noise: -log(-log(u)) in FP64.
+__device__ __forceinline__ double gumbel64(uint32_t w) { return -log(-log(uniform64(w))); }
+
+// FP32 noise. -log(u) comes from log(u) for u < 1/2 and from log1p(-(1-u)) for
+// u >= 1/2, with 1-u formed from the complement of the word, so the large-noise
+// tail keeps the word's full resolution. Its distance from the FP64 value is at
+// most GUMBEL_ERR * (1 + |G|) for every 32-bit word (checked exhaustively on the
+// device by tests/test_gumbel_bound.py).
+constexpr float GUMBEL_ERR = 1.9073486e-06f;  // 2^-19
+constexpr float GUMBEL_MAX = 22.875f;          // above the largest noise, 22.87386
+__device__ __forceinline__ float gumbel32(uint32_t w) {
+  const float e = w < 0x80000000u ? -logf((float(w) + 0.5f) * 2.3283064365386963e-10f)
+                                  : -log1pf(-(float(~w) + 0.5f) * 2.3283064365386963e-10f);
+  return -logf(e);
+}
+// A cheap upper bound on the same noise: -log(u) >= 1 - u, and the native
+// base-2 log with a relative margin. Checked to bound G for every word.
+__device__ __forceinline__ float gumbel_upper(uint32_t w) {
+  const float e = w < 0x80000000u ? -__logf((float(w) + 0.5f) * 2.3283064365386963e-10f)
+                                  : (float(~w) + 0.5f) * 2.3283064365386963e-10f;
+  const float g = -__logf(e * (1.f - 4e-6f));
+  return g + 4e-6f * (1.f + fabsf(g));
+}
+
+// ---------------------------------------------------------------------------
+// Unsigned keys in value order; -0 and +0 get the same key (the oracle compares
+// values, and -0 == +0).
+__device__ __forceinline__ uint32_t order_key(float v) {
+  const uint32_t b = __float_as_uint(v == 0.f ? 0.f : v);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ uint64_t order_key(double v) {
+  const uint64_t b = uint64_t(__double_as_longlong(v == 0.0 ? 0.0 : v));
+  return (b >> 63) ? ~b : (b | (uint64_t(1) << 63));
+}
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+__device__ __forceinline__ double key_value(uint64_t k) {
+  return __longlong_as_double((long long)((k >> 63) ? (k & ~(uint64_t(1) << 63)) : ~k));
+}
+
+// (value desc, id asc): does a come before b?
+template <class W> __device__ __forceinline__ bool before(W av, int ai, W bv, int bi) {
+  return av > bv || (av == bv && ai < bi);
+}
+
+// ---------------------------------------------------------------------------
+// Double-double arithmetic for exact-looking FP64 sums.
+struct DD { double hi, lo; };
+__device__ __forceinline__ DD dd_add(DD a, DD b) {
+  const double s = a.hi + b.hi;
+  const double v = s - a.hi;
+  const double e = (a.hi - (s - v)) + (b.hi - v);
+  const double lo = (a.lo + b.lo) + e;
+  const double hi = s + lo;
+  return DD{hi, lo - (hi - s)};
+}
+__device__ __forceinline__ DD xshfl(DD d, int m) { return DD{xshfl(d.hi, m), xshfl(d.lo, m)}; }
+
+// The correctly rounded value of a non-negative DD sum whose exact value lies
+// within `err` of hi + lo, if that is certain. Returns false when the exact sum
+// may round to a neighbour (then the caller computes it exactly).
+__device__ __forceinline__ bool dd_round_certain(DD s, double err, double* out) {
+  const double hi = s.hi;
+  if (!(hi > 0) || !isfinite(hi)) { *out = hi; return hi == 0 && err == 0; }
+  const double up = nextafter(hi, INFINITY) - hi;
+  const double down = hi - nextafter(hi, 0.0);
+  const bool ok = s.lo + err < 0.5 * up && s.lo - err > -0.5 * down;
+  *out = hi;
+  return ok;
+}
+
+// Relative error bound of a DD sum of n non-negative terms formed by dd_add in any
+// order, plus an absolute allowance for terms near the subnormal range.
+__device__ __forceinline__ double dd_sum_error(DD s, double n) {
+  return n * 0x1p-100 * s.hi + n * 0x1p-1060;
+}
+
+}  // namespace es

@@ -1,0 +1,1783 @@
+// exactsample_amd device code: sampling and speculative-draft verification on gfx950.
+//
+// One launch per call (es_launch). The grid has two kinds of 256-thread blocks:
+//
+//  * request blocks (the first ceil(R / 256)): validate each request's
+//    metadata and write the outputs of every request that fails it
+//    (reference: csrc/verify/verify.cu:6-56, initialize);
+//  * slice blocks (rows x slices): one pass over a slice of a row held in
+//    registers: validation (NaN/+inf anywhere), the valid count, the two
+//    largest valid logits, and, for rows a list can finish, every valid logit
+//    at or above a threshold chosen so that the slice's top L are stored
+//    (reference: fused.cuh:409-519 row_stats, :686-798 row_hist/row_gather).
+//    The last slice block of a row to arrive merges the slices in slice order
+//    and finishes the row:
+//      - failed and greedy rows directly;
+//      - list rows (top-k <= list_max, small top-p nuclei) from the merged
+//        candidates, in FP64 with the oracle's formulas, the whole block
+//        working (reference: fused.cuh:1250-1412);
+//      - every other row on the full-row path, re-reading the row: exact
+//        radix cuts, exact top-p boundary, certified FP32 draws with FP64
+//        rescoring (reference: fused.cuh:1446-1810).
+//    The block that completes a request's last row commits the request
+//    (reference: verify.cu:169-217, finalize).
+//
+// Results never depend on the slice count, the slot or the arrival order:
+// merges run in slice order, candidate sets are exact up to a recorded
+// frontier and are sorted before use, and every decision is either exact or
+// certified with a bound and otherwise recomputed in FP64.
+#include "es_device.h"
+#include "es_layout.h"
+#include "es_superacc.h"
+#include "es_plan.h"
+#include <limits.h>
+#include <type_traits>
+#include <stdio.h>
+
+namespace es {
+
+constexpr float X_ERR = 4.8e-7f;          // |x32 - x| <= X_ERR * |x|; |w32/w - 1| <= X_ERR * (1 + |x|)
+constexpr float SCORE_ERR = 1.9073486e-06f;  // |s32 - s| <= SCORE_ERR * (1 + |x| + |G|)
+constexpr float PRUNE_MARGIN = 1e-3f;
+constexpr float SUM_PRUNE = -40.f;        // weights below e^-40 are bounded, not summed
+constexpr double SUM_PRUNE_W = 4.25e-18;  // e^-40 rounded up
+constexpr int TOPP_SLICE_NEED = 64;       // candidates per slice for a top-p list
+constexpr int LIST_LIMIT = 1024;          // largest candidate union the merge takes
+constexpr int HEAD_BINS = 256;            // quarter-logit bins below the maximum for the union's head
+constexpr int TOPP_HEAD = 96;             // entries a top-p list sorts first
+
+// ---------------------------------------------------------------------------
+// Element types.
+template <int DT> struct Ty;
+template <> struct Ty<ES_F32> { using T = float; using W = float; using Key = uint32_t; };
+template <> struct Ty<ES_F64> { using T = double; using W = double; using Key = uint64_t; };
+template <> struct Ty<ES_BF16> { using T = uint16_t; using W = float; using Key = uint32_t; };
+template <> struct Ty<ES_F16> { using T = uint16_t; using W = float; using Key = uint32_t; };
+
+template <int DT> __device__ __forceinline__ typename Ty<DT>::W widen(typename Ty<DT>::T x);
+template <> __device__ __forceinline__ float widen<ES_F32>(float x) { return x; }
+template <> __device__ __forceinline__ double widen<ES_F64>(double x) { return x; }
+template <> __device__ __forceinline__ float widen<ES_BF16>(uint16_t x) { return __uint_as_float(uint32_t(x) << 16); }
+template <> __device__ __forceinline__ float widen<ES_F16>(uint16_t x) {
+  _Float16 h;
+  __builtin_memcpy(&h, &x, 2);
+  return float(h);
+}
+
+template <class W> __device__ __forceinline__ W neg_inf() { return W(-INFINITY); }
+
+// One row of logits; tokens are read in groups of four (one Philox block).
+template <int DT, bool VEC> struct RowView {
+  using T = typename Ty<DT>::T;
+  using W = typename Ty<DT>::W;
+  const T* base;
+  int64_t stride;
+  int vocab;
+  __device__ __forceinline__ RowView(const es_matrix& m, int64_t row, int vocab_)
+      : base(static_cast<const T*>(m.data) + row * m.s0), stride(m.s1), vocab(vocab_) {}
+  __device__ __forceinline__ void load(int g, W v[4]) const {
+    const int t = 4 * g;
+    if constexpr (VEC) {
+      if constexpr (DT == ES_F32) {
+        const float4 x = *reinterpret_cast<const float4*>(base + t);
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+      } else if constexpr (DT == ES_F64) {
+        const double2 x = reinterpret_cast<const double2*>(base + t)[0];
+        const double2 y = reinterpret_cast<const double2*>(base + t)[1];
+        v[0] = x.x; v[1] = x.y; v[2] = y.x; v[3] = y.y;
+      } else {
+        const uint2 x = *reinterpret_cast<const uint2*>(base + t);
+        v[0] = widen<DT>(uint16_t(x.x)); v[1] = widen<DT>(uint16_t(x.x >> 16));
+        v[2] = widen<DT>(uint16_t(x.y)); v[3] = widen<DT>(uint16_t(x.y >> 16));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = t + j < vocab ? widen<DT>(base[int64_t(t + j) * stride]) : neg_inf<W>();
+    }
+  }
+  __device__ __forceinline__ W value(int t) const { return widen<DT>(base[int64_t(t) * stride]); }
+};
+
+// ---------------------------------------------------------------------------
+// Argument access.
+__device__ __forceinline__ int64_t at(const es_vec_i64& v, int64_t i) { return v.data[i * v.stride]; }
+__device__ __forceinline__ double at(const es_vec_f64& v, int64_t i) { return v.data[i * v.stride]; }
+__device__ __forceinline__ int64_t draft_at(const es_arguments& a, int64_t req, int64_t i) {
+  return a.draft_ids[req * a.draft_s0 + i * a.draft_s1];
+}
+// Bits j of group g: is token 4g + j allowed by the mask?
+__device__ __forceinline__ uint32_t group_bits(const es_arguments& a, int64_t row, int g) {
+  if (!a.mask) return 0xfu;
+  const int t = 4 * g;
+  if (t >= a.vocab) return 0u;
+  return (uint32_t(a.mask[row * a.mask_s0 + int64_t(t >> 5) * a.mask_s1]) >> (t & 31)) & 0xfu;
+}
+__device__ __forceinline__ bool allowed(const es_arguments& a, int64_t row, int t) {
+  return !a.mask || ((uint32_t(a.mask[row * a.mask_s0 + int64_t(t >> 5) * a.mask_s1]) >> (t & 31)) & 1u);
+}
+
+__device__ __forceinline__ uint8_t* row_region(const es_arguments& a, int64_t row) {
+  return a.workspace + HEADER_BYTES + row * ROW_BYTES;
+}
+__device__ __forceinline__ RowResult* row_result(const es_arguments& a, int64_t row) {
+  return reinterpret_cast<RowResult*>(row_region(a, row) + OFF_RESULT);
+}
+__device__ __forceinline__ RowState* row_state(const es_arguments& a, int64_t row) {
+  return reinterpret_cast<RowState*>(row_region(a, row) + OFF_STATE);
+}
+__device__ __forceinline__ Counters* counters(const es_arguments& a, int64_t row) {
+  return reinterpret_cast<Counters*>(row_region(a, row) + OFF_COUNTERS);
+}
+__device__ __forceinline__ SlicePart* slice_parts(const es_arguments& a, int64_t row) {
+  return reinterpret_cast<SlicePart*>(row_region(a, row) + OFF_PARTS);
+}
+template <class W> __device__ __forceinline__ Cand<W>* candidates(const es_arguments& a, int64_t row) {
+  return reinterpret_cast<Cand<W>*>(row_region(a, row) + OFF_CAND);
+}
+
+// ---------------------------------------------------------------------------
+// Metadata (reference verify.cu:6-40; oracle reference.py:177-196).
+__device__ __forceinline__ bool offsets_malformed(const es_arguments& a) {
+  int bad = 0;
+  if (threadIdx.x == 0) bad = at(a.cu_rows, 0) != 0 || at(a.cu_rows, a.requests) != a.rows;
+  for (int64_t i = threadIdx.x; i < a.requests; i += BLOCK) {
+    const int64_t x = at(a.cu_rows, i), y = at(a.cu_rows, i + 1);
+    bad |= x < 0 || y > a.rows || x > y;
+  }
+  return __syncthreads_or(bad) != 0;
+}
+
+__device__ __forceinline__ int32_t metadata_status(const es_arguments& a, int64_t req, bool malformed) {
+  if (malformed) return ES_INVALID_INPUT;
+  const int64_t begin = at(a.cu_rows, req), end = at(a.cu_rows, req + 1);
+  if (begin < 0 || end > a.rows || end <= begin || end - begin > a.max_draft + 1) return ES_INVALID_INPUT;
+  const double t = at(a.temperature, req), p = at(a.top_p, req), m = at(a.min_p, req);
+  const int64_t k = at(a.top_k, req), kind = at(a.draft_kind, req), stream = at(a.stream, req);
+  if (!isfinite(t) || t < 0 || !isfinite(p) || p <= 0 || p > 1 || !isfinite(m) || m < 0 || m > 1 ||
+      k < 0 || k > a.vocab || kind < 0 || kind > 1)
+    return ES_INVALID_INPUT;
+  if ((a.mode == 1 && kind == 1) || (kind == 1 && end - begin > 1 && !a.draft.data) || stream < 0 ||
+      uint64_t(stream) > 0xffffffffull)
+    return ES_INVALID_INPUT;
+  for (int64_t row = begin; row < end; ++row) {
+    const int64_t pos = at(a.position, row);
+    if (pos < 0 || uint64_t(pos) > 0xffffffffull) return ES_INVALID_INPUT;
+    if (row + 1 < end) {
+      const int64_t id = draft_at(a, req, row - begin);
+      if (id < 0 || id >= a.vocab) return ES_INVALID_INPUT;
+    }
+  }
+  return ES_OK;
+}
+
+// The request owning a row of a well-formed batch: the last one starting at or before it.
+__device__ __forceinline__ int64_t request_of(const es_arguments& a, int64_t row) {
+  int64_t lo = 0, hi = a.requests - 1;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) / 2;
+    if (at(a.cu_rows, mid) <= row) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+__device__ __forceinline__ void write_failed_request(const es_arguments& a, int64_t req, int32_t status, int32_t path) {
+  int64_t* tokens = a.tokens + req * a.token_s0;
+  for (int64_t i = 0; i <= a.max_draft; ++i) tokens[i * a.token_s1] = -1;
+  a.accepted[req * a.accepted_s] = 0;
+  a.status[req * a.status_s] = status;
+  a.path[req * a.path_s] = path;
+}
+
+// Cross-block data. Blocks of one row or request run on different XCDs, whose
+// L2 caches are not coherent with each other. Everything one block writes for
+// another is stored with device-scope (write-through, sc1) atomic stores and
+// read with device-scope atomic loads, so no agent-scope fence (an L2
+// write-back and invalidate per block) is needed. Ordering comes from waiting
+// for the stores to be acknowledged (vmcnt(0)) before the arrival atomic.
+__device__ __forceinline__ void st_dev(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_dev(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev32(int32_t* p, int32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t ld_dev32(const int32_t* p) {
+  return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T> __device__ __forceinline__ void publish(T* dst, const T& v) {
+  static_assert(sizeof(T) % 8 == 0, "published in 8-byte words");
+  uint64_t w[sizeof(T) / 8];
+  __builtin_memcpy(w, &v, sizeof(T));
+#pragma unroll
+  for (size_t i = 0; i < sizeof(T) / 8; ++i) st_dev(reinterpret_cast<uint64_t*>(dst) + i, w[i]);
+}
+template <class T> __device__ __forceinline__ T fetch(const T* src) {
+  static_assert(sizeof(T) % 8 == 0, "fetched in 8-byte words");
+  uint64_t w[sizeof(T) / 8];
+#pragma unroll
+  for (size_t i = 0; i < sizeof(T) / 8; ++i) w[i] = ld_dev(reinterpret_cast<const uint64_t*>(src) + i);
+  T v;
+  __builtin_memcpy(&v, w, sizeof(T));
+  return v;
+}
+// Every thread's outstanding stores acknowledged (s_waitcnt vmcnt(0)).
+__device__ __forceinline__ void stores_done() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Arrival on a counter; true in every thread of the block that arrives last,
+// which also resets the counter and may then fetch what the others published.
+__device__ __forceinline__ bool arrive(uint32_t* counter, uint32_t expected, int* s_flag) {
+  stores_done();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t old = atomicAdd(counter, 1u);
+    const int last = old + 1 == expected;
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = last;
+  }
+  __syncthreads();
+  return *s_flag != 0;
+}
+
+// ---------------------------------------------------------------------------
+// Shared memory of a block (one union; each phase uses one member).
+template <class W> struct Shared {
+  union {
+    struct {
+      W red_w[WAVES];
+      W red_w2[WAVES];
+      int red_i[WAVES];
+      int red_i2[WAVES];
+      double red_d[WAVES];
+    } r;
+    struct {
+      W v[LIST_LIMIT];
+      int id[LIST_LIMIT];
+      W sv[LIST_LIMIT];
+      int sid[LIST_LIMIT];
+      double w[LIST_LIMIT];
+    } list;
+    struct {
+      unsigned cnt[2048];
+      double mass[2048];
+    } hist;
+  } u;
+  double dred[WAVES];
+  DD ddred[WAVES];
+  int ired[WAVES];
+  float fred[WAVES];
+  unsigned long long limbs[SACC_LIMBS];
+  int flag;
+  int n;
+  // Merged row statistics and parameters, broadcast to the block.
+  double maximum, runner_up, frontier, sum, err;
+  int greedy, runner_up_id, valid, bad, n_cand_total, pruned, frontier_id;
+  int n_cand[MAX_SLICES];
+  int req_found;
+  int64_t req;
+  int32_t status;
+  int pick;
+  unsigned __int128 ck;
+};
+
+// The request's parameters, read once per block.
+struct Params {
+  int64_t req, begin, end;
+  double temperature, top_p, min_p;
+  int64_t top_k;
+  int32_t status;
+  int draft_row, verify, coupled, full_q, draft_id;
+  RngAddr rng;
+};
+
+// The row's request and its parameters, checked by the whole block: the
+// offsets are scanned once (malformed check and owner lookup together) and the
+// per-row checks of the request run one row per thread, so the prologue is a
+// few independent load rounds rather than a dependent chain.
+template <class SH>
+__device__ __forceinline__ void block_params(const es_arguments& a, int64_t row, Params* p, SH& sh) {
+  const int tid = threadIdx.x;
+  if (tid == 0) sh.req_found = -1;
+  __syncthreads();
+  int bad = 0;
+  if (tid == 0) bad = at(a.cu_rows, 0) != 0 || at(a.cu_rows, a.requests) != a.rows;
+  for (int64_t i = tid; i < a.requests; i += BLOCK) {
+    const int64_t x = at(a.cu_rows, i), y = at(a.cu_rows, i + 1);
+    bad |= x < 0 || y > a.rows || x > y;
+    if (x <= row && row < y) sh.req_found = int(i);
+  }
+  const bool malformed = __syncthreads_or(bad) != 0;
+  if (malformed || sh.req_found < 0) {
+    if (tid == 0) p->status = ES_INVALID_INPUT;
+    __syncthreads();
+    return;
+  }
+  const int64_t req = sh.req_found;
+  const int64_t begin = at(a.cu_rows, req), end = at(a.cu_rows, req + 1);
+  int mbad = end - begin > a.max_draft + 1;
+  if (!mbad) {
+    if (tid == 0) {
+      const double t = at(a.temperature, req), pp = at(a.top_p, req), m = at(a.min_p, req);
+      const int64_t k = at(a.top_k, req), kind = at(a.draft_kind, req), stream = at(a.stream, req);
+      mbad |= !isfinite(t) || t < 0 || !isfinite(pp) || pp <= 0 || pp > 1 || !isfinite(m) || m < 0 || m > 1 ||
+              k < 0 || k > a.vocab || kind < 0 || kind > 1;
+      mbad |= (a.mode == 1 && kind == 1) || (kind == 1 && end - begin > 1 && !a.draft.data) || stream < 0 ||
+              uint64_t(stream) > 0xffffffffull;
+    }
+    for (int64_t r = begin + tid; r < end; r += BLOCK) {
+      const int64_t pos = at(a.position, r);
+      mbad |= pos < 0 || uint64_t(pos) > 0xffffffffull;
+      if (r + 1 < end) {
+        const int64_t id = draft_at(a, req, r - begin);
+        mbad |= id < 0 || id >= a.vocab;
+      }
+    }
+  }
+  mbad = __syncthreads_or(mbad);
+  if (tid == 0) {
+    p->req = req;
+    p->status = mbad ? ES_INVALID_INPUT : ES_OK;
+    if (!mbad) {
+      p->begin = begin;
+      p->end = end;
+      p->temperature = at(a.temperature, req);
+      p->top_p = at(a.top_p, req);
+      p->min_p = at(a.min_p, req);
+      p->top_k = at(a.top_k, req);
+      p->draft_row = row + 1 < end;
+      p->coupled = a.mode == 1;
+      p->verify = p->draft_row && !p->coupled;
+      p->full_q = p->draft_row && at(a.draft_kind, req) == 1;
+      p->draft_id = p->draft_row ? int(draft_at(a, req, row - begin)) : -1;
+      p->rng.seed = uint64_t(at(a.seed, req));
+      p->rng.stream = uint32_t(at(a.stream, req));
+      p->rng.position = uint32_t(at(a.position, row));
+    }
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// The commit of one request from its rows' results (reference verify.cu:169-217),
+// run by one wave. Lane l takes rows begin + l, begin + l + 64, ...
+__device__ __forceinline__ void finalize_request(const es_arguments& a, int64_t req) {
+  const int lane = lane_id();
+  const int64_t begin = at(a.cu_rows, req), end = at(a.cu_rows, req + 1);
+  int64_t* tokens = a.tokens + req * a.token_s0;
+  for (int pass = 0; pass < 2; ++pass) {
+    for (int64_t base = begin; base < end; base += WAVE) {
+      const int64_t row = base + lane;
+      int s = ES_OK;
+      if (row < end) {
+        const RowResult rr = fetch(row_result(a, row));
+        s = pass == 0 ? rr.target_status : rr.status;
+      }
+      const uint64_t bad = __ballot(s != ES_OK);
+      if (bad) {
+        const int first = __shfl(s, __ffsll((unsigned long long)bad) - 1, WAVE);
+        for (int64_t i = lane; i <= a.max_draft; i += WAVE) tokens[i * a.token_s1] = -1;
+        if (lane == 0) {
+          a.accepted[req * a.accepted_s] = 0;
+          a.status[req * a.status_s] = first;
+          a.path[req * a.path_s] = ES_PATH_FUSED;
+        }
+        return;
+      }
+    }
+  }
+  const uint64_t seed = uint64_t(at(a.seed, req));
+  const uint32_t stream = uint32_t(at(a.stream, req));
+  int64_t stop = end - 1;
+  for (int64_t base = begin; base < end - 1; base += WAVE) {
+    const int64_t row = base + lane;
+    bool reject = false;
+    if (row < end - 1) {
+      const RowResult r = fetch(row_result(a, row));
+      const int64_t draft = draft_at(a, req, row - begin);
+      if (a.mode == 1) {
+        reject = r.sample != draft;
+      } else {
+        const Words w = philox(seed, stream, uint32_t(at(a.position, row)), 1u, 0u);
+        reject = !(uniform64(w.w[0]) < fmin(1.0, r.p / r.q));
+      }
+    }
+    const uint64_t rejected = __ballot(reject);
+    if (rejected) { stop = base + __ffsll((unsigned long long)rejected) - 1; break; }
+  }
+  const RowResult r = fetch(row_result(a, stop));
+  const int token = stop == end - 1 || a.mode == 1 ? r.sample : r.residual;
+  const int64_t accepted = stop - begin;
+  const bool empty = stop < end - 1 && token < 0;  // an impossible rejection: invalid, never a token
+  for (int64_t i = lane; i <= a.max_draft; i += WAVE) {
+    int64_t t = -1;
+    if (!empty) t = i < accepted ? draft_at(a, req, i) : i == accepted ? int64_t(token) : -1;
+    tokens[i * a.token_s1] = t;
+  }
+  if (lane == 0) {
+    a.accepted[req * a.accepted_s] = empty ? 0 : int32_t(accepted);
+    a.status[req * a.status_s] = empty ? ES_INVALID_INPUT : ES_OK;
+    a.path[req * a.path_s] = ES_PATH_FUSED;
+  }
+}
+
+// Every row arrives once per call; the last one totals the rows' FP64
+// recomputations into workspace word 1.
+template <class W> __device__ __forceinline__ void grid_arrive(const es_arguments& a, Shared<W>& sh) {
+  if (arrive(&counters(a, 0)->grid, uint32_t(a.rows), &sh.flag)) {
+    unsigned total = 0;
+    for (int64_t r = threadIdx.x; r < a.rows; r += BLOCK) total += unsigned(ld_dev32(&row_state(a, r)->fallbacks));
+    total = block_all(total, [](unsigned x, unsigned y) { return x + y; }, reinterpret_cast<unsigned*>(sh.ired));
+    if (threadIdx.x == 0) reinterpret_cast<uint32_t*>(a.workspace)[1] = total;
+  }
+}
+
+// Publishes a finished row and runs the request commit and the call's
+// fallback total when this row completes them. Every thread calls it.
+template <class W>
+__device__ __forceinline__ void complete_row(const es_arguments& a, int64_t row, const Params& p,
+                                             const RowResult& result, int fallbacks, int route, Shared<W>& sh) {
+  if (threadIdx.x == 0) {
+    if (p.end - p.begin > 1) publish(row_result(a, row), result);  // read by the request's finalize
+    RowState* st = row_state(a, row);
+    st->part = PART_DONE;
+    st->route = route;
+    st_dev32(&st->fallbacks, fallbacks);
+  }
+  const int64_t nrows = p.end - p.begin;
+  if (nrows == 1) {
+    // A request of one row (no drafts) is committed from the result in hand.
+    if (threadIdx.x <= a.max_draft) {
+      const bool ok = result.status == ES_OK;
+      a.tokens[p.req * a.token_s0 + threadIdx.x * a.token_s1] = threadIdx.x == 0 && ok ? result.sample : -1;
+    }
+    for (int64_t i = int64_t(threadIdx.x) + BLOCK; i <= a.max_draft; i += BLOCK) a.tokens[p.req * a.token_s0 + i * a.token_s1] = -1;
+    if (threadIdx.x == 0) {
+      a.accepted[p.req * a.accepted_s] = 0;
+      a.status[p.req * a.status_s] = result.status;
+      a.path[p.req * a.path_s] = ES_PATH_FUSED;
+    }
+  } else if (arrive(&counters(a, p.begin)->request, uint32_t(nrows), &sh.flag)) {
+    if (wave_id() == 0) finalize_request(a, p.req);
+  }
+  grid_arrive(a, sh);
+}
+
+template <class W>
+__device__ __forceinline__ void skip_row(const es_arguments& a, int64_t row, Shared<W>& sh) {
+  if (threadIdx.x == 0) {
+    RowState* st = row_state(a, row);
+    st->part = PART_SKIP;
+    st_dev32(&st->fallbacks, 0);
+  }
+  grid_arrive(a, sh);
+}
+
+// ---------------------------------------------------------------------------
+// Temperature arithmetic shared by the list and full-row parts.
+template <class W> struct Temp {
+  double M, T, min_p;
+  float inv_t, ln_min_p, min_p_tol;
+  bool slow;
+  __device__ __forceinline__ void init(double maximum, double temperature, double min_p_) {
+    M = maximum; T = temperature; min_p = min_p_;
+    inv_t = float(1.0 / temperature);
+    slow = !(inv_t < 1e30f);
+    ln_min_p = min_p > 0 ? float(log(min_p)) : -INFINITY;
+    min_p_tol = min_p > 0 ? 1e-6f * (1.f + fabsf(ln_min_p)) : 0.f;
+  }
+  // The oracle's x = (l - max) / T in FP64 (reference.py:63).
+  __device__ __forceinline__ double x64(W v) const { return (double(v) - M) / T; }
+  // FP32 x with |x32 - x| <= X_ERR * |x|.
+  __device__ __forceinline__ float x32(W v) const {
+    if constexpr (sizeof(W) == 8) {
+      return float(x64(v));
+    } else {
+      const float d = v - float(M);
+      return slow ? float(double(d) / T) : d * inv_t;
+    }
+  }
+  // exp(x) >= min_p and exp(x) > 0 for the FP64 x, settled in FP32 when x is
+  // clear of both thresholds and in FP64 otherwise.
+  __device__ __forceinline__ bool kept(W v, float x) const {
+    if (x > -744.f && fabsf(x - ln_min_p) > X_ERR * fabsf(x) + min_p_tol) return x > ln_min_p;
+    if (x < -745.2f) return false;
+    const double w = exp(x64(v));
+    return w > 0 && w >= min_p;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Composite order keys: larger means earlier in (logit desc, ID asc) order.
+typedef unsigned __int128 u128;
+template <class W> struct CK;
+template <> struct CK<float> {
+  static constexpr int BITS = 64;
+  __device__ static __forceinline__ u128 make(float v, int id) {
+    return u128((uint64_t(order_key(v)) << 32) | uint64_t(~uint32_t(id)));
+  }
+  __device__ static __forceinline__ float value(u128 ck) { return key_value(uint32_t(uint64_t(ck) >> 32)); }
+};
+template <> struct CK<double> {
+  static constexpr int BITS = 96;
+  __device__ static __forceinline__ u128 make(double v, int id) { return (u128(order_key(v)) << 32) | u128(~uint32_t(id)); }
+  __device__ static __forceinline__ double value(u128 ck) { return key_value(uint64_t(ck >> 32)); }
+};
+__device__ __forceinline__ int ck_id(u128 ck) { return int(~uint32_t(uint64_t(ck))); }
+
+// ---------------------------------------------------------------------------
+// Bin of an entry d logits below the row maximum: quarter-logit bins, the last
+// one for everything 63.75 or more below. Monotone in d, so a prefix of bins
+// holds a prefix of the (value desc) order.
+__device__ __forceinline__ int head_bin(double d) {
+  return d < double(HEAD_BINS - 1) / 4 ? int(d * 4) : HEAD_BINS - 1;
+}
+
+// FP64 draws over a sorted list in LDS: argmax of log(p_i) + G_i with the
+// oracle's formula (reference.py:94-104), lowest ID on ties; -1 when empty.
+template <class W>
+__device__ __forceinline__ int list_draw(const Params& p, Shared<W>& sh, int n, int sub, int excluded) {
+  double best = -INFINITY;
+  int best_id = INT_MAX;
+  for (int i = threadIdx.x; i < n; i += BLOCK) {
+    const int id = sh.u.list.sid[i];
+    const double pi = sh.u.list.w[i];
+    if (id == excluded || !(pi > 0)) continue;
+    const double s = log(pi) + gumbel64(word_of(p.rng, uint32_t(sub), uint32_t(id)));
+    if (s > best || (s == best && id < best_id)) { best = s; best_id = id; }
+  }
+  // Reduce (score, id) across the block.
+  struct SI { double s; int id; };
+  SI v{best, best_id};
+  auto op = [](SI x, SI y) { return (y.s > x.s || (y.s == x.s && y.id < x.id)) ? y : x; };
+#pragma unroll
+  for (int m = WAVE / 2; m; m >>= 1) {
+    SI o{xshfl(v.s, m), xshfl(v.id, m)};
+    v = op(v, o);
+  }
+  __syncthreads();
+  if (lane_id() == 0) { sh.dred[wave_id()] = v.s; sh.ired[wave_id()] = v.id; }
+  __syncthreads();
+  SI r{sh.dred[0], sh.ired[0]};
+  for (int w = 1; w < WAVES; ++w) r = op(r, SI{sh.dred[w], sh.ired[w]});
+  __syncthreads();
+  return r.id == INT_MAX ? -1 : r.id;
+}
+
+// DD sum over the block in thread order (deterministic for a fixed block shape).
+template <class W> __device__ __forceinline__ DD block_dd(DD v, Shared<W>& sh) {
+  return block_all(v, [](DD x, DD y) { return dd_add(x, y); }, sh.ddred);
+}
+
+// The correctly rounded sum of sh.u.list.w[0, n): certified DD, else exact.
+template <class W> __device__ __forceinline__ double list_fsum(Shared<W>& sh, int n, int* fallbacks) {
+  DD acc{0, 0};
+  for (int i = threadIdx.x; i < n; i += BLOCK) acc = dd_add(acc, DD{sh.u.list.w[i], 0});
+  acc = block_dd(acc, sh);
+  double r;
+  if (dd_round_certain(acc, dd_sum_error(acc, n), &r)) return r;
+  sacc_clear(sh.limbs);
+  __syncthreads();
+  for (int i = threadIdx.x; i < n; i += BLOCK) sacc_add(sh.limbs, sh.u.list.w[i]);
+  __syncthreads();
+  if (threadIdx.x == 0) { sh.dred[0] = sacc_round(sh.limbs); ++*fallbacks; }
+  __syncthreads();
+  r = sh.dred[0];
+  __syncthreads();
+  return r;
+}
+
+// Does round(P) reach t, for P known as a DD within err? 1 yes, 0 no, -1 not certain.
+__device__ __forceinline__ int dd_reaches(DD P, double err, double t) {
+  const double below = nextafter(t, 0.0);
+  const DD lo = dd_add(P, DD{-t, 0});       // P - t
+  if (lo.hi - err >= 0) return 1;           // P >= t
+  const DD lo2 = dd_add(P, DD{-below, 0});  // P - pred(t)
+  if (lo2.hi + err < 0) return 0;           // P < pred(t)
+  return -1;
+}
+
+// Finishes a list row from the candidates of its slices. Returns false when the
+// candidates cannot settle the row; the full-row path then takes it.
+// The kept set is a prefix of (logit desc, ID asc) order: min-p and positivity
+// remove a suffix, top-k keeps a prefix and top-p keeps a prefix.
+template <class W>
+__device__ __forceinline__ bool list_finish(const es_arguments& a, int64_t row, const Params& p, Shared<W>& sh, int slices,
+                            int cap_slice, bool topk_mode, int n_keep, RowResult* result, int* fallbacks,
+                                              int* why) {
+  // Every valid token at or before (F, F_id) in (value desc, ID asc) order
+  // is among the candidates; sorted, they are the exact head of the order.
+  const double F = sh.frontier;
+  const int F_id = sh.frontier_id;
+  if (!(F < INFINITY)) { *why = 1; return false; }
+  if (threadIdx.x == 0) sh.n = 0;
+  __syncthreads();
+  const Cand<W>* cands = candidates<W>(a, row);
+  const int total_slots = slices * cap_slice;
+  for (int idx = threadIdx.x; idx < total_slots; idx += BLOCK) {
+    const int s = idx / cap_slice, i = idx - s * cap_slice;
+    if (i >= sh.n_cand[s]) continue;
+    const Cand<W> c = fetch(cands + idx);
+    if (!(double(c.v) > F || (double(c.v) == F && c.id <= F_id))) continue;
+    const int slot = atomicAdd(&sh.n, 1);
+    if (slot < LIST_LIMIT) { sh.u.list.v[slot] = c.v; sh.u.list.id[slot] = c.id; }
+  }
+  __syncthreads();
+  const int n_u = sh.n;
+  __syncthreads();
+  if (n_u > LIST_LIMIT || n_u == 0) { *why = 2; return false; }
+  if (topk_mode && n_u < n_keep) { *why = 3; return false; }
+  // Only the head of the union is needed: bin the entries by distance below
+  // the row maximum (quarter-logit bins) and keep the bins up to the one that
+  // completes the first `want` entries; rank-sort just those.
+  const int want = topk_mode ? n_keep : min(n_u, TOPP_HEAD);
+  const double M0 = sh.maximum;
+  unsigned* bins = reinterpret_cast<unsigned*>(sh.u.list.sid);  // HEAD_BINS counters
+  for (int i = threadIdx.x; i < HEAD_BINS; i += BLOCK) bins[i] = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < n_u; i += BLOCK)
+    atomicAdd(&bins[head_bin(M0 - double(sh.u.list.v[i]))], 1u);
+  __syncthreads();
+  int cut_bin = HEAD_BINS - 1;
+  {
+    const int c = threadIdx.x < HEAD_BINS ? int(bins[threadIdx.x]) : 0;
+    int tot;
+    const int incl = block_scan_add(c, sh.ired, &tot);
+    if (threadIdx.x < HEAD_BINS && incl >= want && incl - c < want) sh.pick = int(threadIdx.x);
+    __syncthreads();
+    cut_bin = sh.pick;
+    __syncthreads();
+  }
+  // Compact the head entries into (sv, sid), rank-sort them into (v, id),
+  // and copy the sorted head back to (sv, sid).
+  if (threadIdx.x == 0) sh.n = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < n_u; i += BLOCK) {
+    const W x = sh.u.list.v[i];
+    if (head_bin(M0 - double(x)) <= cut_bin) {
+      const int slot = atomicAdd(&sh.n, 1);
+      sh.u.list.sv[slot] = x;
+      sh.u.list.sid[slot] = sh.u.list.id[i];
+    }
+  }
+  __syncthreads();
+  const int n_h = sh.n;  // every entry outside the head comes after all of these
+  const bool whole_union = n_h == n_u;
+  const int n_out = topk_mode ? n_keep : n_h;
+  // Rank sort: each thread ranks its entries against all n_h, four loads in flight.
+  for (int i = threadIdx.x; i < n_h; i += BLOCK) {
+    const W vi = sh.u.list.sv[i];
+    const int ii = sh.u.list.sid[i];
+    int rank = 0, j = 0;
+    for (; j + 4 <= n_h; j += 4) {
+      const W v0 = sh.u.list.sv[j], v1 = sh.u.list.sv[j + 1], v2 = sh.u.list.sv[j + 2], v3 = sh.u.list.sv[j + 3];
+      const int d0 = sh.u.list.sid[j], d1 = sh.u.list.sid[j + 1], d2 = sh.u.list.sid[j + 2], d3 = sh.u.list.sid[j + 3];
+      rank += before(v0, d0, vi, ii) + before(v1, d1, vi, ii) + before(v2, d2, vi, ii) + before(v3, d3, vi, ii);
+    }
+    for (; j < n_h; ++j) rank += before(sh.u.list.sv[j], sh.u.list.sid[j], vi, ii);
+    if (rank < n_out) { sh.u.list.v[rank] = vi; sh.u.list.id[rank] = ii; }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < n_out; i += BLOCK) {
+    sh.u.list.sv[i] = sh.u.list.v[i];
+    sh.u.list.sid[i] = sh.u.list.id[i];
+  }
+  __syncthreads();
+  // FP64 weights with the oracle's formula, and the min-p/positivity cut.
+  const double M = sh.maximum, T = p.temperature;
+  int first_out = INT_MAX;
+  for (int i = threadIdx.x; i < n_out; i += BLOCK) {
+    const double w = exp((double(sh.u.list.sv[i]) - M) / T);
+    sh.u.list.w[i] = w;
+    if (!(w >= p.min_p && w > 0.0)) first_out = min(first_out, i);
+  }
+  first_out = block_all(first_out, [](int x, int y) { return x < y ? x : y; }, sh.ired);
+  const int n1 = min(n_out, first_out);
+  int n2 = n1;
+  if (p.top_p < 1) {
+    double lo_t, hi_t;
+    const bool whole = topk_mode || (whole_union && n_u == sh.valid);  // the list is the whole kept set
+    if (whole) {
+      const double total = list_fsum(sh, n1, fallbacks);
+      lo_t = hi_t = p.top_p * total;
+    } else {
+      if (!(sh.err >= 0) || !(sh.sum - sh.err > 0)) { *why = 4; return false; }
+      lo_t = p.top_p * (sh.sum - sh.err) * (1 - 1e-15);
+      hi_t = p.top_p * (sh.sum + sh.err) * (1 + 1e-15);
+    }
+    // Inclusive DD prefix sums: thread t owns entries [4t, 4t + 4).
+    constexpr int PER = LIST_LIMIT / BLOCK;
+    DD local{0, 0};
+    for (int u = 0; u < PER; ++u) {
+      const int i = PER * threadIdx.x + u;
+      if (i < n1) local = dd_add(local, DD{sh.u.list.w[i], 0});
+    }
+    // Exclusive scan of the per-thread sums in thread order.
+    DD incl = local;
+    const int lane = lane_id();
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+      const DD y{__shfl_up(incl.hi, o, WAVE), __shfl_up(incl.lo, o, WAVE)};
+      if (lane >= o) incl = dd_add(y, incl);
+    }
+    __syncthreads();
+    if (lane == WAVE - 1) sh.ddred[wave_id()] = incl;
+    __syncthreads();
+    DD before_w{0, 0};
+    for (int w = 0; w < wave_id(); ++w) before_w = dd_add(before_w, sh.ddred[w]);
+    const DD excl_t = dd_add(before_w, dd_add(incl, DD{-local.hi, -local.lo}));
+    int first_lo = INT_MAX, first_hi = INT_MAX, unsure = INT_MAX;
+    DD run = excl_t;
+    for (int u = 0; u < PER; ++u) {
+      const int i = PER * threadIdx.x + u;
+      if (i >= n1) break;
+      run = dd_add(run, DD{sh.u.list.w[i], 0});
+      const double err = dd_sum_error(run, i + 1) + 4 * 0x1p-104 * run.hi;
+      const int rl = dd_reaches(run, err, lo_t), rh = dd_reaches(run, err, hi_t);
+      if (rl != 0) first_lo = min(first_lo, i);
+      if (rh != 0) first_hi = min(first_hi, i);
+      if (rl < 0 || rh < 0) unsure = min(unsure, i);
+    }
+    auto mn = [](int x, int y) { return x < y ? x : y; };
+    first_lo = block_all(first_lo, mn, sh.ired);
+    first_hi = block_all(first_hi, mn, sh.ired);
+    unsure = block_all(unsure, mn, sh.ired);
+    if (unsure <= first_hi || first_lo != first_hi) { *why = 5; return false; }
+    if (first_hi == INT_MAX) {
+      if (!whole) { *why = 6; return false; }  // the nucleus may extend past the list
+      n2 = n1;
+    } else {
+      n2 = first_hi + 1;
+    }
+  }
+  const double den = list_fsum(sh, n2, fallbacks);
+  for (int i = threadIdx.x; i < n2; i += BLOCK) sh.u.list.w[i] = sh.u.list.w[i] / den;
+  __syncthreads();
+  RowResult r{0, 1, -1, -1, ES_OK, ES_OK};
+  if (p.verify) {
+    int at_draft = INT_MAX;
+    for (int i = threadIdx.x; i < n2; i += BLOCK)
+      if (sh.u.list.sid[i] == p.draft_id) at_draft = i;
+    at_draft = block_all(at_draft, [](int x, int y) { return x < y ? x : y; }, sh.ired);
+    const double px = at_draft == INT_MAX ? 0.0 : sh.u.list.w[at_draft];
+    const double u = uniform64(word_of(p.rng, 1u, 0u));
+    const bool accept = u < fmin(1.0, px);
+    r.p = accept ? 1.0 : 0.0;
+    if (!accept) r.residual = list_draw(p, sh, n2, 2, p.draft_id);
+  } else {
+    r.sample = list_draw(p, sh, n2, 0, -1);
+  }
+  *result = r;
+  return true;
+}
+
+// ---------------------------------------------------------------------------
+// Full-row path: one block re-reads the row (and the proposal row) as often as
+// it needs. Exact integer cuts, exact (certified or superaccumulated) FP64
+// sums, certified FP32 draws with FP64 rescoring.
+template <int DT, bool VEC> struct FullRow {
+  using W = typename Ty<DT>::W;
+  static constexpr int TG = 8;  // groups of four per thread in flight
+  const es_arguments& a;
+  int64_t row;
+  const Params& p;
+  Shared<W>& sh;
+  RowView<DT, VEC> view, qview;
+  int groups;
+  Temp<W> tp;
+  int fallbacks;
+
+  __device__ __forceinline__ FullRow(const es_arguments& a_, int64_t row_, const Params& p_, Shared<W>& sh_, int groups_)
+      : a(a_), row(row_), p(p_), sh(sh_), view(a_.target, row_, int(a_.vocab)), qview(a_.draft, row_, int(a_.vocab)),
+        groups(groups_), fallbacks(0) {}
+
+  // Calls f(t, v, allowed) for every token of the row (or of the proposal row).
+  template <bool Q, class F> __device__ __forceinline__ void each(F&& f) const {
+    const RowView<DT, VEC>& vw = Q ? qview : view;
+    for (int base = threadIdx.x; base < groups; base += BLOCK * TG) {
+      W v[TG][4];
+      uint32_t bits[TG];
+#pragma unroll
+      for (int u = 0; u < TG; ++u) {
+        const int g = base + u * BLOCK;
+        if (g < groups) {
+          vw.load(g, v[u]);
+          bits[u] = Q ? 0xfu : group_bits(a, row, g);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[u][j] = neg_inf<W>();
+          bits[u] = 0;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < TG; ++u) {
+        const int g = base + u * BLOCK;
+        if (g >= groups) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) f(4 * g + j, v[u][j], ((bits[u] >> j) & 1u) != 0);
+      }
+    }
+  }
+
+  __device__ __forceinline__ bool valid_tok(W v, bool ok) const { return ok && v > neg_inf<W>(); }
+
+  // The correctly rounded sum of f(t, v) over tokens (f returns a weight >= 0,
+  // or 0 to skip); certified DD first, exact superaccumulator otherwise.
+  template <bool Q, class F> __device__ double exact_sum(F&& f, bool count_fallback) {
+    if (count_fallback) ++fallbacks;
+    DD acc{0, 0};
+    int n = 0;
+    each<Q>([&](int t, W v, bool ok) {
+      const double w = f(t, v, ok);
+      if (w > 0) { acc = dd_add(acc, DD{w, 0}); ++n; }
+    });
+    acc = block_dd(acc, sh);
+    n = block_all(n, [](int x, int y) { return x + y; }, sh.ired);
+    double r;
+    if (dd_round_certain(acc, dd_sum_error(acc, n), &r)) return r;
+    sacc_clear(sh.limbs);
+    __syncthreads();
+    each<Q>([&](int t, W v, bool ok) {
+      const double w = f(t, v, ok);
+      if (w > 0) sacc_add(sh.limbs, w);
+    });
+    __syncthreads();
+    if (threadIdx.x == 0) { sh.dred[0] = sacc_round(sh.limbs); }
+    __syncthreads();
+    r = sh.dred[0];
+    __syncthreads();
+    return r;
+  }
+
+  // The n-th (1-based) composite key, in descending order, among tokens where
+  // pred(t, v, ok) holds: radix selection over 11-bit digits of the composite.
+  template <class Pred> __device__ u128 select_nth(int n, Pred&& pred) {
+    constexpr int NB = CK<W>::BITS;
+    constexpr int D = 11;
+    u128 prefix = 0;
+    int known = 0, need = n;
+    while (known < NB) {
+      const int width = min(D, NB - known), shift = NB - known - width;
+      const int buckets = 1 << width;
+      for (int i = threadIdx.x; i < buckets; i += BLOCK) sh.u.hist.cnt[i] = 0;
+      __syncthreads();
+      each<false>([&](int t, W v, bool ok) {
+        if (!pred(t, v, ok)) return;
+        const u128 ck = CK<W>::make(v, t);
+        if (known && (ck >> (NB - known)) != prefix) return;
+        atomicAdd(&sh.u.hist.cnt[int(ck >> shift) & (buckets - 1)], 1u);
+      });
+      __syncthreads();
+      // Descending digits: thread t owns buckets [buckets - 1 - PER t - u].
+      const int per = (buckets + BLOCK - 1) / BLOCK;
+      int local = 0;
+      for (int u = 0; u < per; ++u) {
+        const int d = buckets - 1 - (per * threadIdx.x + u);
+        if (d >= 0) local += int(sh.u.hist.cnt[d]);
+      }
+      int total;
+      const int incl = block_scan_add(local, sh.ired, &total);
+      int run = incl - local;
+      for (int u = 0; u < per; ++u) {
+        const int d = buckets - 1 - (per * threadIdx.x + u);
+        if (d < 0) break;
+        const int c = int(sh.u.hist.cnt[d]);
+        if (run < need && run + c >= need) { sh.pick = d; sh.n = run; sh.flag = c; }
+        run += c;
+      }
+      __syncthreads();
+      const int d = sh.pick, count = sh.flag;
+      need -= sh.n;
+      __syncthreads();
+      prefix = (prefix << width) | u128(d);
+      known += width;
+      if (count == 1 && known < NB) {  // a unique token: read its whole key
+        each<false>([&](int t, W v, bool ok) {
+          if (!pred(t, v, ok)) return;
+          const u128 ck = CK<W>::make(v, t);
+          if ((ck >> (NB - known)) == prefix) sh.ck = ck;
+        });
+        __syncthreads();
+        const u128 r = sh.ck;
+        __syncthreads();
+        return r;
+      }
+    }
+    return prefix;
+  }
+
+  // The first composite key (descending order) among tokens where pred holds at
+  // which the correctly rounded running sum of weight(t, v) reaches target.
+  template <class Pred, class Wt> __device__ u128 mass_boundary(double target, Pred&& pred, Wt&& weight) {
+    constexpr int NB = CK<W>::BITS;
+    constexpr int D = 11;
+    u128 prefix = 0;
+    int known = 0;
+    double base_lo = 0, base_hi = 0;  // exact mass before the current region
+    const double below_t = nextafter(target, 0.0);
+    while (known < NB) {
+      const int width = min(D, NB - known), shift = NB - known - width;
+      const int buckets = 1 << width;
+      for (int i = threadIdx.x; i < buckets; i += BLOCK) { sh.u.hist.cnt[i] = 0; sh.u.hist.mass[i] = 0; }
+      __syncthreads();
+      each<false>([&](int t, W v, bool ok) {
+        if (!pred(t, v, ok)) return;
+        const u128 ck = CK<W>::make(v, t);
+        if (known && (ck >> (NB - known)) != prefix) return;
+        const int d = int(ck >> shift) & (buckets - 1);
+        atomicAdd(&sh.u.hist.cnt[d], 1u);
+        atomicAdd(&sh.u.hist.mass[d], weight(t, v));
+      });
+      __syncthreads();
+      const int per = (buckets + BLOCK - 1) / BLOCK;
+      // Walk buckets in descending order with interval bounds.
+      double local = 0, local_err = 0;
+      for (int u = 0; u < per; ++u) {
+        const int d = buckets - 1 - (per * threadIdx.x + u);
+        if (d < 0) break;
+        const double m = sh.u.hist.mass[d];
+        local += m;
+        local_err += double(sh.u.hist.cnt[d]) * 0x1p-52 * m;
+      }
+      // Exclusive prefix over threads (FP64, fixed order) with a generous bound.
+      double incl = local, incl_e = local_err;
+      const int lane = lane_id();
+#pragma unroll
+      for (int o = 1; o < WAVE; o <<= 1) {
+        const double y = __shfl_up(incl, o, WAVE), ye = __shfl_up(incl_e, o, WAVE);
+        if (lane >= o) { incl += y; incl_e += ye; }
+      }
+      __syncthreads();
+      if (lane == WAVE - 1) { sh.dred[wave_id()] = incl; reinterpret_cast<double*>(sh.ddred)[wave_id()] = incl_e; }
+      __syncthreads();
+      double before_m = 0, before_e = 0;
+      for (int w = 0; w < wave_id(); ++w) { before_m += sh.dred[w]; before_e += reinterpret_cast<double*>(sh.ddred)[w]; }
+      double run = before_m + incl - local, run_e = before_e + incl_e - local_err;
+      int first = INT_MAX, first_sure = INT_MAX;
+      for (int u = 0; u < per; ++u) {
+        const int d = buckets - 1 - (per * threadIdx.x + u);
+        if (d < 0) break;
+        const int c = int(sh.u.hist.cnt[d]);
+        const double m = sh.u.hist.mass[d];
+        run += m;
+        run_e += double(c) * 0x1p-52 * m;
+        if (c == 0) continue;
+        const double slack = run_e + 1e-15 * run + 1e-300;
+        const double hi = base_hi + run + slack, lo = base_lo + run - slack;
+        const int rank = per * threadIdx.x + u;  // position in descending order
+        if (!(hi < below_t)) first = min(first, rank);
+        if (lo >= target) first_sure = min(first_sure, rank);
+      }
+      auto mn = [](int x, int y) { return x < y ? x : y; };
+      first = block_all(first, mn, sh.ired);
+      first_sure = block_all(first_sure, mn, sh.ired);
+      if (first == INT_MAX) {
+        // Rounding never reaches the target inside this region: take its last token.
+        first = first_sure = INT_MAX - 1;
+      }
+      int chosen = -1;
+      int rank = first;
+      while (chosen < 0) {
+        if (rank == INT_MAX - 1) {  // last nonempty bucket of the region
+          int last = -1;
+          for (int d = threadIdx.x; d < buckets; d += BLOCK)
+            if (sh.u.hist.cnt[d]) last = max(last, buckets - 1 - d);
+          last = block_all(last, [](int x, int y) { return x > y ? x : y; }, sh.ired);
+          chosen = last;
+          break;
+        }
+        if (rank == first_sure) { chosen = rank; break; }
+        // Not certain: the exact rounded mass through the end of this bucket.
+        const int d = buckets - 1 - rank;
+        const u128 end_ck = ((prefix << width) | u128(d)) << shift;  // lowest key of bucket d
+        const double through = exact_sum<false>([&](int t, W v, bool ok) -> double {
+          if (!pred(t, v, ok)) return 0.0;
+          return CK<W>::make(v, t) >= end_ck ? weight(t, v) : 0.0;
+        }, true);
+        if (through >= target) { chosen = rank; break; }
+        // Move to the next nonempty bucket.
+        int next = INT_MAX;
+        for (int dd = threadIdx.x; dd < buckets; dd += BLOCK) {
+          const int r = buckets - 1 - dd;
+          if (r > rank && sh.u.hist.cnt[dd]) next = min(next, r);
+        }
+        next = block_all(next, mn, sh.ired);
+        if (next == INT_MAX) { chosen = rank; break; }  // cannot happen: the region reaches the target
+        rank = next;
+      }
+      const int d = buckets - 1 - chosen;
+      const int count = int(sh.u.hist.cnt[d]);
+      // Mass before bucket d inside the region, with its bound.
+      double mb = 0, mbe = 0;
+      for (int dd = threadIdx.x; dd < buckets; dd += BLOCK)
+        if (dd > d) { mb += sh.u.hist.mass[dd]; mbe += double(sh.u.hist.cnt[dd]) * 0x1p-52 * sh.u.hist.mass[dd]; }
+      mb = block_all(mb, [](double x, double y) { return x + y; }, sh.dred);
+      mbe = block_all(mbe, [](double x, double y) { return x + y; }, sh.dred);
+      const double slack = mbe + 1e-15 * mb + 1e-300;
+      base_lo = base_lo + mb - slack;
+      base_hi = base_hi + mb + slack;
+      __syncthreads();
+      prefix = (prefix << width) | u128(d);
+      known += width;
+      if (count == 1 && known < NB) {
+        each<false>([&](int t, W v, bool ok) {
+          if (!pred(t, v, ok)) return;
+          const u128 ck = CK<W>::make(v, t);
+          if ((ck >> (NB - known)) == prefix) sh.ck = ck;
+        });
+        __syncthreads();
+        const u128 r = sh.ck;
+        __syncthreads();
+        return r;
+      }
+    }
+    return prefix;
+  }
+
+  // Certified FP32 draw over tokens where in(t, v, ok) holds (excluded
+  // removed), FP64 rescoring when the certificate fails. floor_id is a token
+  // certainly in the set (or -1).
+  template <class In> __device__ int draw(int sub, int excluded, int floor_id, In&& in) {
+    if (threadIdx.x == 0) {
+      float floor = -INFINITY;
+      if (floor_id >= 0) {
+        const W v = view.value(floor_id);
+        const float x = tp.x32(v);
+        const float g = gumbel32(word_of(p.rng, uint32_t(sub), uint32_t(floor_id)));
+        floor = x + g - SCORE_ERR * (1.f + fabsf(x) + fabsf(g));
+      }
+      sh.fred[0] = floor;
+    }
+    __syncthreads();
+    const float floor = sh.fred[0];
+    __syncthreads();
+    float best_mid = -INFINITY, best_lo = -INFINITY, best_hi = -INFINITY, others = -INFINITY;
+    int best_id = INT_MAX;
+    float bar = floor - PRUNE_MARGIN;
+    each<false>([&](int t, W v, bool ok) {
+      if (t == excluded || !in(t, v, ok)) return;
+      const float x = tp.x32(v);
+      const float ub = x + GUMBEL_MAX + SCORE_ERR * (1.f + fabsf(x) + GUMBEL_MAX);
+      if (ub < bar) { others = fmaxf(others, ub); return; }
+      const uint32_t w = word_of(p.rng, uint32_t(sub), uint32_t(t));
+      const float gb = gumbel_upper(w);
+      const float ub2 = x + gb + SCORE_ERR * (1.f + fabsf(x) + fabsf(gb));
+      if (ub2 < bar) { others = fmaxf(others, ub2); return; }
+      const float G = gumbel32(w), s = x + G, e = SCORE_ERR * (1.f + fabsf(x) + fabsf(G));
+      if (s > best_mid || (s == best_mid && t < best_id)) {
+        others = fmaxf(others, best_hi);
+        best_mid = s; best_lo = s - e; best_hi = s + e; best_id = t;
+      } else {
+        others = fmaxf(others, s + e);
+      }
+      bar = fmaxf(bar, best_lo - PRUNE_MARGIN);
+    });
+    // Block merge of the certified picks.
+    struct Pk { float mid, lo, hi, others; int id; };
+    Pk pk{best_mid, best_lo, best_hi, others, best_id};
+    auto op = [](Pk x, Pk y) {
+      const bool yw = y.mid > x.mid || (y.mid == x.mid && y.id < x.id);
+      Pk w = yw ? y : x, l = yw ? x : y;
+      w.others = fmaxf(fmaxf(x.others, y.others), l.hi);
+      return w;
+    };
+#pragma unroll
+    for (int m = WAVE / 2; m; m >>= 1) {
+      Pk o{xshfl(pk.mid, m), xshfl(pk.lo, m), xshfl(pk.hi, m), xshfl(pk.others, m), xshfl(pk.id, m)};
+      pk = op(pk, o);
+    }
+    __shared__ Pk s_pk[WAVES];
+    __syncthreads();
+    if (lane_id() == 0) s_pk[wave_id()] = pk;
+    __syncthreads();
+    Pk r = s_pk[0];
+    for (int w = 1; w < WAVES; ++w) r = op(r, s_pk[w]);
+    __syncthreads();
+    if (r.id == INT_MAX) return -1;
+    if (r.lo > r.others) return r.id;
+    // FP64 rescoring of every token whose upper bound reaches the winner's lower bound.
+    ++fallbacks;
+    const float threshold = r.lo;
+    double best = -INFINITY;
+    int bid = INT_MAX;
+    each<false>([&](int t, W v, bool ok) {
+      if (t == excluded || !in(t, v, ok)) return;
+      const float x = tp.x32(v);
+      const float ub = x + GUMBEL_MAX + SCORE_ERR * (1.f + fabsf(x) + GUMBEL_MAX);
+      if (ub < threshold) return;
+      const uint32_t w = word_of(p.rng, uint32_t(sub), uint32_t(t));
+      const float gb = gumbel_upper(w);
+      if (x + gb + SCORE_ERR * (1.f + fabsf(x) + fabsf(gb)) < threshold) return;
+      const double s = tp.x64(v) + gumbel64(w);
+      if (s > best || (s == best && t < bid)) { best = s; bid = t; }
+    });
+    struct SI { double s; int id; };
+    SI si{best, bid};
+    auto op2 = [](SI x, SI y) { return (y.s > x.s || (y.s == x.s && y.id < x.id)) ? y : x; };
+#pragma unroll
+    for (int m = WAVE / 2; m; m >>= 1) si = op2(si, SI{xshfl(si.s, m), xshfl(si.id, m)});
+    __syncthreads();
+    if (lane_id() == 0) { sh.dred[wave_id()] = si.s; sh.ired[wave_id()] = si.id; }
+    __syncthreads();
+    SI res{sh.dred[0], sh.ired[0]};
+    for (int w = 1; w < WAVES; ++w) res = op2(res, SI{sh.dred[w], sh.ired[w]});
+    __syncthreads();
+    return res.id == INT_MAX ? -1 : res.id;
+  }
+
+  // Finishes the row. Greedy rows without a full proposal and failed rows
+  // never come here.
+  __device__ RowResult run(double maximum, int greedy, int runner_up_id, int valid) {
+    RowResult r{0, 1, -1, -1, ES_OK, ES_OK};
+    const bool full_q = p.full_q != 0;
+    // ---- The actual proposal q of a full-q draft row (reference.py:206-216). ----
+    double qmax = -INFINITY, sq = 0, wq_draft = 0;
+    if (full_q) {
+      int qbad = 0, qvalid = 0;
+      W qm = neg_inf<W>();
+      each<true>([&](int, W y, bool) {
+        qbad |= isnan(y) || y == W(INFINITY);
+        qvalid += y > neg_inf<W>();
+        qm = y > qm ? y : qm;
+      });
+      qbad = block_all(qbad, [](int x, int y) { return x | y; }, sh.ired);
+      qvalid = block_all(qvalid, [](int x, int y) { return x + y; }, sh.ired);
+      qm = block_all(qm, [](W x, W y) { return x > y ? x : y; }, sh.u.r.red_w);
+      int qstatus = qbad ? ES_INVALID_INPUT : qvalid == 0 ? ES_NO_VALID_TOKEN : ES_OK;
+      qmax = double(qm);
+      if (qstatus == ES_OK) {
+        // sq = fsum over q's support of exp(y - qmax) (no filters, T = 1).
+        sq = exact_sum<true>([&](int, W y, bool) -> double {
+          return y > neg_inf<W>() ? exp(double(y) - qmax) : 0.0;
+        }, false);
+        const W yd = qview.value(p.draft_id);
+        wq_draft = yd > neg_inf<W>() ? exp(double(yd) - qmax) : 0.0;
+        if (!(wq_draft / sq > 0)) qstatus = ES_DRAFT_ZERO_PROB;
+      }
+      if (qstatus != ES_OK) { r.status = qstatus; return r; }
+    }
+    auto qprob = [&](int t) -> double {
+      const W y = qview.value(t);
+      return y > neg_inf<W>() ? exp(double(y) - qmax) / sq : 0.0;
+    };
+    // ---- Greedy full-q rows: p is a point mass at the greedy token. ----
+    if (p.temperature == 0) {
+      r.sample = greedy;
+      if (p.verify) {
+        const double qx = wq_draft / sq;
+        const double px = p.draft_id == greedy ? 1.0 : 0.0;
+        const double u = uniform64(word_of(p.rng, 1u, 0u));
+        const bool accept = u < fmin(1.0, px / qx);
+        r.p = accept ? 1.0 : 0.0;
+        if (!accept) r.residual = fmax(1.0 - qprob(greedy), 0.0) > 0 ? greedy : -1;
+      }
+      return r;
+    }
+    tp.init(maximum, p.temperature, p.min_p);
+    // ---- Kept set: valid, min-p and positivity (a prefix of the order). ----
+    auto kept = [&](int, W v, bool ok) { return valid_tok(v, ok) && tp.kept(v, tp.x32(v)); };
+    int nk = 0;
+    each<false>([&](int t, W v, bool ok) { nk += kept(t, v, ok); });
+    nk = block_all(nk, [](int x, int y) { return x + y; }, sh.ired);
+    // ---- Top-k: an exact cut at the k-th token (reference.py:67-71). ----
+    u128 cut = 0;  // keep ck >= cut
+    if (p.top_k > 0 && p.top_k < nk) cut = select_nth(int(p.top_k), kept);
+    auto in_k = [&](int t, W v, bool ok) { return kept(t, v, ok) && CK<W>::make(v, t) >= cut; };
+    auto w64 = [&](int, W v) -> double { return exp(tp.x64(v)); };
+    double den = 0;
+    bool den_exact = false;
+    // ---- Top-p: the shortest prefix whose fsum reaches top_p * fsum(all) (reference.py:73-85). ----
+    if (p.top_p < 1) {
+      const double total = exact_sum<false>([&](int t, W v, bool ok) -> double {
+        return in_k(t, v, ok) ? w64(t, v) : 0.0;
+      }, false);
+      const double target = p.top_p * total;
+      cut = mass_boundary(target, in_k, w64);
+      den = exact_sum<false>([&](int t, W v, bool ok) -> double {
+        return in_k(t, v, ok) && CK<W>::make(v, t) >= cut ? w64(t, v) : 0.0;
+      }, false);
+      den_exact = true;
+    }
+    auto in_final = [&](int t, W v, bool ok) { return in_k(t, v, ok) && CK<W>::make(v, t) >= cut; };
+    // The floor of a draw: the first token of the order that the draw may take.
+    const int floor_token = greedy;
+    // ---- Ratio test (reference.py:229-230). ----
+    if (p.verify) {
+      const W vx = view.value(p.draft_id);
+      const bool x_in = in_final(p.draft_id, vx, allowed(a, row, p.draft_id));
+      const double u = uniform64(word_of(p.rng, 1u, 0u));
+      bool accept = false;
+      if (x_in) {
+        if (!den_exact) {
+          // FP32 sum of kept weights with its bound first.
+          float s = 0, c = 0, e = 0;
+          int pruned = 0;
+          each<false>([&](int t, W v, bool ok) {
+            if (!in_final(t, v, ok)) return;
+            const float x = tp.x32(v);
+            if (x < SUM_PRUNE) { ++pruned; return; }
+            const float w = expf(x), d = w - c, tt = s + d;
+            c = (tt - s) - d; s = tt;
+            e += w * (X_ERR * (1.f + fabsf(x)));
+          });
+          const double sum = block_all(double(s) - double(c), [](double x, double y) { return x + y; }, sh.dred);
+          const double et = block_all(double(e), [](double x, double y) { return x + y; }, sh.dred);
+          pruned = block_all(pruned, [](int x, int y) { return x + y; }, sh.ired);
+          const double esp = 1.01 * et + 4.8e-7 * sum + pruned * SUM_PRUNE_W;
+          const double wx = exp(tp.x64(vx));
+          const double qx_lo = full_q ? wq_draft / sq * (1 - 1e-15) : 1.0, qx_hi = full_q ? wq_draft / sq * (1 + 1e-15) : 1.0;
+          const double rlo = fmin(1.0, wx / (sum + esp) / qx_hi) * (1 - 1e-12);
+          const double rhi = fmin(1.0, wx / (sum - esp) / qx_lo) * (1 + 1e-12);
+          const bool bounded = esp >= 0 && sum - esp > 0;
+          if (bounded && u < rlo) accept = true;
+          else if (bounded && u >= rhi) accept = false;
+          else {
+            den = exact_sum<false>([&](int t, W v, bool ok) -> double { return in_final(t, v, ok) ? w64(t, v) : 0.0; }, false);
+            den_exact = true;
+            ++fallbacks;
+            accept = u < fmin(1.0, (wx / den) / (full_q ? wq_draft / sq : 1.0));
+          }
+        } else {
+          const double px = exp(tp.x64(vx)) / den;
+          accept = u < fmin(1.0, px / (full_q ? wq_draft / sq : 1.0));
+        }
+      }
+      r.p = accept ? 1.0 : 0.0;
+      if (accept) return r;
+      if (!full_q) {
+        const int floor_id = p.draft_id == greedy ? (runner_up_id != INT_MAX ? runner_up_id : -1) : greedy;
+        int fl = floor_id;
+        if (fl >= 0 && fl != greedy) {
+          const W vf = view.value(fl);
+          if (!in_final(fl, vf, allowed(a, row, fl))) fl = -1;
+        }
+        r.residual = draw(2, p.draft_id, fl, in_final);
+        return r;
+      }
+      // Full-q residual max(p - q, 0) in FP64 over the kept set (reference.py:236).
+      if (!den_exact) {
+        den = exact_sum<false>([&](int t, W v, bool ok) -> double { return in_final(t, v, ok) ? w64(t, v) : 0.0; }, false);
+        den_exact = true;
+      }
+      double best = -INFINITY;
+      int bid = INT_MAX;
+      each<false>([&](int t, W v, bool ok) {
+        if (!in_final(t, v, ok)) return;
+        const double pr = exp(tp.x64(v)) / den;
+        const double rr = fmax(pr - qprob(t), 0.0);
+        if (!(rr > 0)) return;
+        const double s = log(rr) + gumbel64(word_of(p.rng, 2u, uint32_t(t)));
+        if (s > best || (s == best && t < bid)) { best = s; bid = t; }
+      });
+      struct SI { double s; int id; };
+      SI si{best, bid};
+      auto op2 = [](SI x, SI y) { return (y.s > x.s || (y.s == x.s && y.id < x.id)) ? y : x; };
+#pragma unroll
+      for (int m = WAVE / 2; m; m >>= 1) si = op2(si, SI{xshfl(si.s, m), xshfl(si.id, m)});
+      __syncthreads();
+      if (lane_id() == 0) { sh.dred[wave_id()] = si.s; sh.ired[wave_id()] = si.id; }
+      __syncthreads();
+      SI res{sh.dred[0], sh.ired[0]};
+      for (int w = 1; w < WAVES; ++w) res = op2(res, SI{sh.dred[w], sh.ired[w]});
+      __syncthreads();
+      r.residual = res.id == INT_MAX ? -1 : res.id;
+      return r;
+    }
+    r.sample = draw(0, -1, floor_token, in_final);
+    return r;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Register-tile helpers of the slice pass. Token (i, j) of a thread is
+// 4 * (gb + BLOCK * i) + j; IDs rise with (i, thread, j).
+
+// One bit per token of the tile where pred(value, id) holds.
+template <class W, int G, class Pred>
+__device__ __forceinline__ uint64_t collect_bits(const W (&v)[G][4], Pred&& pred, int gb = 0) {
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = 4 * i + j;
+      const uint32_t bit = pred(v[i][j], 4 * (gb + BLOCK * i) + j) && v[i][j] > neg_inf<W>();
+      if (k < 32) lo |= bit << k; else hi |= bit << (k - 32);
+    }
+  }
+  return (uint64_t(hi) << 32) | lo;
+}
+
+// The slice's L-th valid token in (value desc, ID asc) order, given that at
+// least L valid tokens are >= floor: radix selection over the value's order
+// key among those tokens, then the tie broken by ID in (i, thread, j) order.
+template <class W, int G>
+__device__ void slice_cut(const W (&v)[G][4], int gb, int L, W floor, Shared<W>& sh, W* out_v, int* out_id) {
+  using K = typename std::conditional<sizeof(W) == 8, uint64_t, uint32_t>::type;
+  constexpr int KB = int(sizeof(K) * 8);
+  // Scratch in the block's union: 256 counters, then G x BLOCK tie counts.
+  unsigned* hist = reinterpret_cast<unsigned*>(&sh.u);
+  static_assert(sizeof(sh.u) >= (256 + G * BLOCK) * sizeof(int), "slice_cut scratch");
+  K prefix = 0, known = 0;
+  int need = L;
+  for (int shift = KB - 8; shift >= 0; shift -= 8) {
+    __syncthreads();
+    hist[threadIdx.x] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const W x = v[i][j];
+        if (x >= floor && x > neg_inf<W>()) {
+          const K k = order_key(x);
+          if ((k & known) == prefix) atomicAdd(&hist[int(k >> shift) & 255], 1u);
+        }
+      }
+    }
+    __syncthreads();
+    const int c = int(hist[255 - threadIdx.x]);  // descending digits, one per thread
+    int tot;
+    const int incl = block_scan_add(c, sh.ired, &tot);
+    if (incl >= need && incl - c < need) { sh.pick = 255 - int(threadIdx.x); sh.n = incl - c; }
+    __syncthreads();
+    need -= sh.n;
+    prefix |= K(sh.pick) << shift;
+    known |= K(255) << shift;
+  }
+  const W cut_v = key_value(prefix);
+  // `need` tokens with value cut_v are taken, the lowest IDs first.
+  int* ties = reinterpret_cast<int*>(&sh.u) + 256;  // [G][BLOCK]
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c += v[i][j] == cut_v;
+    ties[i * BLOCK + threadIdx.x] = c;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int before = 0, gi = 0;
+    for (; gi < G; ++gi) {
+      int s = 0;
+      for (int t = 0; t < BLOCK; ++t) s += ties[gi * BLOCK + t];
+      if (before + s >= need) break;
+      before += s;
+    }
+    int t = 0;
+    for (; t < BLOCK; ++t) {
+      const int c = ties[gi * BLOCK + t];
+      if (before + c >= need) break;
+      before += c;
+    }
+    sh.pick = gi;
+    sh.n = t;
+    sh.flag = need - before;  // the rank of the last taken tie inside that thread's group
+  }
+  __syncthreads();
+  const int gi = sh.pick, owner = sh.n, rank = sh.flag;
+  __syncthreads();
+  if (int(threadIdx.x) == owner) {
+    int seen = 0, id = INT_MAX;
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      if (i != gi) continue;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (v[i][j] == cut_v && ++seen == rank) id = 4 * (gb + BLOCK * i) + j;
+    }
+    sh.ck = id;
+  }
+  __syncthreads();
+  *out_v = cut_v;
+  *out_id = int(sh.ck);
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// The kernel.
+template <int DT, bool VEC, int G>
+__global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
+  using W = typename Ty<DT>::W;
+  __shared__ Shared<W> sh;
+  __shared__ Params sp;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+
+  // ---- Request blocks. ----
+  if (int(blockIdx.x) < pl.req_blocks) {
+    const bool malformed = offsets_malformed(a);
+    if (blockIdx.x == 0 && tid == 0) {
+      reinterpret_cast<int32_t*>(a.workspace)[0] = malformed;
+      if (a.rows == 0) reinterpret_cast<uint32_t*>(a.workspace)[1] = 0;
+    }
+    const int64_t req = int64_t(blockIdx.x) * BLOCK + tid;
+    if (req < a.requests) {
+      const int32_t st = metadata_status(a, req, malformed);
+      if (st != ES_OK) write_failed_request(a, req, st, ES_PATH_FUSED);
+    }
+    return;
+  }
+
+  // ---- Slice blocks. ----
+  const int b = int(blockIdx.x) - pl.req_blocks;
+  const int64_t row = b / pl.slices;
+  const int slice = b - int(row) * pl.slices;
+  const int vocab = int(a.vocab);
+  const RowView<DT, VEC> view(a.target, row, vocab);
+  const int g0 = slice * pl.gps, g1 = min(g0 + pl.gps, pl.groups);
+
+  // Loads first: the metadata checks below overlap them. Every lane loads (an
+  // index clamped into the row), so there is no branch per load; tokens
+  // outside the slice are then set to -inf.
+  W v[G][4];
+  uint64_t mbits = ~0ull;
+  const int gb = g0 + tid;
+#pragma unroll
+  for (int i = 0; i < G; ++i) view.load(min(gb + BLOCK * i, pl.groups - 1), v[i]);
+  if (a.mask) {
+    mbits = 0;
+#pragma unroll
+    for (int i = 0; i < G; ++i) mbits |= uint64_t(group_bits(a, row, min(gb + BLOCK * i, pl.groups - 1))) << (4 * i);
+  }
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const bool in = gb + BLOCK * i < g1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[i][j] = in ? v[i][j] : neg_inf<W>();
+  }
+  block_params(a, row, &sp, sh);
+  const Params p = sp;
+  if (p.status != ES_OK) {
+    if (slice == 0) skip_row(a, row, sh);
+    return;
+  }
+
+  // ---- Statistics: NaN/+inf anywhere (even masked), valid count, maximum. ----
+  int bad_l = 0, valid_l = 0;
+  W mx = neg_inf<W>();
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bad_l |= isnan(v[i][j]) || v[i][j] == W(INFINITY);
+  }
+  if (a.mask) {
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[i][j] = ((mbits >> (4 * i + j)) & 1ull) ? v[i][j] : neg_inf<W>();
+    }
+  }
+  // From here on a token is valid exactly when its value is above -inf (a NaN
+  // token only occurs in an invalid row, whose other results are unused).
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      valid_l += v[i][j] > neg_inf<W>();
+      mx = v[i][j] > mx ? v[i][j] : mx;
+    }
+  }
+  const int valid_w = wave_all(valid_l, [](int x, int y) { return x + y; });
+  const int bad_w = wave_all(bad_l, [](int x, int y) { return x | y; });
+  if (lane == 0) { sh.u.r.red_i[wave_id()] = valid_w; sh.u.r.red_i2[wave_id()] = bad_w; }
+  const W wmax = wave_all(mx, [](W x, W y) { return x > y ? x : y; });
+  if (lane == 0) sh.u.r.red_w[wave_id()] = wmax;
+  __syncthreads();
+  int valid = 0, bad = 0;
+  W smax = neg_inf<W>();
+  for (int w = 0; w < WAVES; ++w) {
+    valid += sh.u.r.red_i[w];
+    bad |= sh.u.r.red_i2[w];
+    smax = sh.u.r.red_w[w] > smax ? sh.u.r.red_w[w] : smax;
+  }
+  // The lowest ID holding the slice maximum: tokens equal to it are rare, so
+  // the search costs one compare per token behind a wave-uniform branch.
+  int first_id = INT_MAX;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool hit = v[i][j] == smax && smax > neg_inf<W>();
+      first_id = hit && first_id == INT_MAX ? 4 * (gb + BLOCK * i) + j : first_id;
+    }
+  }
+  first_id = block_all(first_id, [](int x, int y) { return x < y ? x : y; }, sh.ired);
+
+  // ---- Candidates for a list row. ----
+  const int list_max = a.list_max;
+  const bool positive_t = p.temperature > 0;
+  int need = 0;  // 0: no candidates; > 0: the slice's top `need`; -1: all valid if they fit
+  if (positive_t && list_max > 0 && !p.full_q && !bad) {
+    if (p.top_k >= 1 && p.top_k <= list_max) need = int(p.top_k);
+    else if (p.top_p < 1 && p.min_p == 0) need = TOPP_SLICE_NEED;
+    else need = -1;
+  }
+  double frontier = -INFINITY, psum = 0, perr = 0;
+  int n_cand = 0, pruned = 0, fid = INT_MAX;
+  if (need != 0) {
+    const int cap = pl.cap_slice;
+    W thr = neg_inf<W>();
+    if (need > 0 && need < valid) {
+      // The j-th largest thread maximum of each wave, j = ceil(L / 4): at least
+      // L valid tokens are >= the smallest of the four (L = min(need, cap)).
+      const int L = min(need, cap);
+      const int j = (L + WAVES - 1) / WAVES;
+      W x = mx;
+#pragma unroll
+      for (int k = 2; k <= WAVE; k <<= 1) {
+#pragma unroll
+        for (int jj = k >> 1; jj > 0; jj >>= 1) {
+          const W y = xshfl(x, jj);
+          const bool lower = (lane & jj) == 0, desc = (lane & k) == 0;
+          const W hi = x > y ? x : y, lo = x > y ? y : x;
+          x = (lower == desc) ? hi : lo;
+        }
+      }
+      const W tw = __shfl(x, j - 1, WAVE);
+      __syncthreads();
+      if (lane == 0) sh.u.r.red_w[wave_id()] = tw;
+      __syncthreads();
+      thr = sh.u.r.red_w[0];
+      for (int w = 1; w < WAVES; ++w) thr = sh.u.r.red_w[w] < thr ? sh.u.r.red_w[w] : thr;
+    }
+    // Tokens at or above the threshold: one bit per token of this thread.
+    // -inf is never taken: the threshold is raised to the lowest finite value.
+    const W take_from = thr > W(-3.4028234663852886e38) ? thr : W(-3.4028234663852886e38);
+    uint64_t take_bits = collect_bits<W, G>(v, [&](W x, int) { return x >= take_from; });
+    int mine = __popcll(take_bits);
+    int total;
+    int offset = block_scan_add(mine, sh.ired, &total) - mine;
+    fid = INT_MAX;  // complete down to (thr, any ID)
+    if (total > cap && need > 0) {
+      // Too many (ties, or a low threshold): take exactly the slice's first L
+      // tokens in (value desc, ID asc) order instead.
+      const int L = min(need, cap);
+      W cut_v;
+      int cut_id;
+      slice_cut<W, G>(v, gb, L, take_from, sh, &cut_v, &cut_id);
+      take_bits = collect_bits<W, G>(v, [&](W x, int t) { return x > cut_v || (x == cut_v && t <= cut_id); }, gb);
+      mine = __popcll(take_bits);
+      offset = block_scan_add(mine, sh.ired, &total) - mine;
+      thr = cut_v;
+      fid = cut_id;
+    }
+    if (total <= cap) {
+      // Few tokens per thread qualify: re-read their values (cache hits)
+      // rather than index the register tile.
+      Cand<W>* out = candidates<W>(a, row) + slice * cap + offset;
+      int o = 0;
+      while (take_bits) {
+        const int k = __ffsll((unsigned long long)take_bits) - 1;
+        take_bits &= take_bits - 1;
+        const int t = 4 * (gb + BLOCK * (k >> 2)) + (k & 3);
+        Cand<W> c{};
+        c.v = view.value(t);
+        c.id = t;
+        publish(out + o, c);
+        ++o;
+      }
+      n_cand = total;
+      // Every valid token of the slice at or before (thr, fid) in (value desc,
+      // ID asc) order is stored.
+      frontier = double(thr);
+    } else {
+      n_cand = 0;
+      frontier = INFINITY;  // nothing certain
+      fid = -1;
+    }
+    // Top-p lists also need the kept weights' sum, relative to the slice maximum.
+    if (need == TOPP_SLICE_NEED && p.top_p < 1 && !(p.top_k >= 1 && p.top_k <= list_max)) {
+      const double ms = double(smax);
+      const float inv_t = float(1.0 / p.temperature);
+      const bool slow = !(inv_t < 1e30f);
+      float s = 0, c = 0, e = 0;
+      int pr = 0;
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const W x = v[i][j];
+          float xl;
+          if constexpr (sizeof(W) == 8) xl = float((double(x) - ms) / p.temperature);
+          else xl = slow ? float(double(x - float(ms)) / p.temperature) : (x - float(ms)) * inv_t;
+          const bool ok = x > neg_inf<W>();
+          const bool counted = ok && xl >= SUM_PRUNE;
+          pr += ok && !counted;
+          const float w = expf(counted ? xl : -100.f) * (counted ? 1.f : 0.f);
+          const float d = w - c, t2 = s + d;
+          c = (t2 - s) - d; s = t2;
+          e += w * (X_ERR * (1.f + fabsf(counted ? xl : 0.f)));
+        }
+      }
+      psum = block_all(double(s) - double(c), [](double x, double y) { return x + y; }, sh.dred);
+      perr = block_all(double(e), [](double x, double y) { return x + y; }, sh.dred);
+      pruned = block_all(pr, [](int x, int y) { return x + y; }, sh.ired);
+    }
+  }
+  if (tid == 0) {
+    SlicePart part;
+    part.max_v = double(smax);
+    part.second_v = -INFINITY;
+    part.frontier = frontier;
+    part.tau = -INFINITY;
+    part.sum = psum;
+    part.err = perr;
+    part.max_id = first_id;
+    part.second_id = fid;  // the frontier's ID
+    part.valid = valid;
+    part.n_cand = n_cand;
+    part.pruned = pruned;
+    part.flags = bad;
+    publish(slice_parts(a, row) + slice, part);
+  }
+  if (!arrive(&counters(a, row)->slices, uint32_t(pl.slices), &sh.flag)) return;
+
+  // ---- The last slice block merges the row (slice order, wave 0). ----
+  if (wave_id() == 0) {
+    SlicePart q;
+    q.max_v = -INFINITY; q.second_v = -INFINITY; q.frontier = -INFINITY; q.tau = -INFINITY;
+    q.sum = 0; q.err = 0; q.max_id = INT_MAX; q.second_id = INT_MAX; q.valid = 0; q.n_cand = 0; q.pruned = 0; q.flags = 0;
+    if (lane < pl.slices) q = fetch(slice_parts(a, row) + lane);
+    if (lane < pl.slices) sh.n_cand[lane] = q.n_cand;
+    struct T2d { double v1; int i1; double v2; int i2; };
+    auto top2d = [](T2d x, T2d y) {
+      const bool yw = before(y.v1, y.i1, x.v1, x.i1);
+      const T2d w = yw ? y : x, l = yw ? x : y;
+      const bool second_l = before(l.v1, l.i1, w.v2, w.i2);
+      return T2d{w.v1, w.i1, second_l ? l.v1 : w.v2, second_l ? l.i1 : w.i2};
+    };
+    T2d t2{q.max_v, q.max_id, q.second_v, q.second_id};
+#pragma unroll
+    for (int m = WAVE / 2; m; m >>= 1) t2 = top2d(t2, T2d{xshfl(t2.v1, m), xshfl(t2.i1, m), xshfl(t2.v2, m), xshfl(t2.i2, m)});
+    const int vsum = wave_all(q.valid, [](int x, int y) { return x + y; });
+    const int bsum = wave_all(q.flags, [](int x, int y) { return x | y; });
+    // The earliest frontier in (value desc, ID asc) order: every slice is
+    // complete down to it.
+    struct Fr { double v; int id; };
+    Fr fr{lane < pl.slices ? q.frontier : -INFINITY, lane < pl.slices ? q.second_id : INT_MAX};
+#pragma unroll
+    for (int m = WAVE / 2; m; m >>= 1) {
+      const Fr o{xshfl(fr.v, m), xshfl(fr.id, m)};
+      fr = (o.v > fr.v || (o.v == fr.v && o.id < fr.id)) ? o : fr;
+    }
+    const int nct = wave_all(q.n_cand, [](int x, int y) { return x + y; });
+    // Top-p sums rescaled from slice maxima to the row maximum (FP64).
+    double s_sum = 0, s_err = 0;
+    int s_pr = q.pruned;
+    if (lane < pl.slices && q.valid > 0 && p.temperature > 0) {
+      const double shift = (t2.v1 - q.max_v) / p.temperature;
+      const double scale = exp(-shift);
+      if (shift > 700) { s_err = (q.sum + q.err) * scale + q.pruned * SUM_PRUNE_W; s_pr = 0; }
+      else { s_sum = q.sum * scale; s_err = (1.01 * q.err + 4.8e-7 * q.sum) * scale * (1 + 1e-14); }
+    }
+    s_sum = wave_all(s_sum, [](double x, double y) { return x + y; });
+    s_err = wave_all(s_err, [](double x, double y) { return x + y; });
+    s_pr = wave_all(s_pr, [](int x, int y) { return x + y; });
+    if (lane == 0) {
+      sh.maximum = t2.v1; sh.greedy = t2.i1; sh.runner_up = t2.v2; sh.runner_up_id = t2.i2;
+      sh.valid = vsum; sh.bad = bsum; sh.frontier = fr.v; sh.frontier_id = fr.id; sh.n_cand_total = nct;
+      sh.sum = s_sum;
+      sh.err = s_err + s_pr * SUM_PRUNE_W + 1e-15 * s_sum;
+    }
+  }
+  __syncthreads();
+  const int status = sh.bad ? ES_INVALID_INPUT : sh.valid == 0 ? ES_NO_VALID_TOKEN : ES_OK;
+  if (tid == 0) {
+    RowState* st = row_state(a, row);
+    st->maximum = sh.maximum; st->runner_up = sh.runner_up; st->greedy = sh.greedy;
+    st->runner_up_id = sh.runner_up_id; st->valid = sh.valid; st->status = status;
+  }
+  RowResult result{0, 1, -1, -1, status, status};
+  int fallbacks = 0, route = 0, why = 0;
+  if (status != ES_OK) {
+    route = 1;
+  } else if (p.temperature == 0 && !p.full_q) {
+    // Greedy: a point mass at the lowest-ID maximum (reference.py:56-58).
+    route = 2;
+    result.sample = sh.greedy;
+    if (p.verify) {
+      const bool accept = p.draft_id == sh.greedy;
+      result.p = accept ? 1.0 : 0.0;
+      if (!accept) result.residual = sh.greedy;
+    }
+  } else {
+    bool done = false;
+    if (p.temperature > 0 && !p.full_q && list_max > 0) {
+      const int valid_all = sh.valid;
+      const int n_keep = p.top_k > 0 && p.top_k < valid_all ? int(p.top_k) : valid_all;
+      const bool topk_list = n_keep <= list_max;
+      const bool topp_list = !topk_list && p.top_p < 1 && n_keep == valid_all && p.min_p == 0;
+      if (topk_list || topp_list) {
+        route = topk_list ? 3 : 4;
+        done = list_finish(a, row, p, sh, pl.slices, pl.cap_slice, topk_list, topk_list ? n_keep : 0, &result,
+                           &fallbacks, &why);
+      }
+    }
+    if (!done) {
+      // The full-row kernel finishes it; it arrives on the counters there.
+      if (tid == 0) {
+        RowState* st = row_state(a, row);
+        st->part = PART_FULL;
+        st->fallbacks = fallbacks;
+        st->route = 100 + why;  // why the list could not finish it (0: not a list row)
+      }
+      return;
+    }
+  }
+  complete_row(a, row, p, result, fallbacks, route, sh);
+}
+
+// ---------------------------------------------------------------------------
+// The full-row kernel: one block per row marked PART_FULL by es_main; every
+// other block returns at once.
+template <int DT, bool VEC>
+__global__ void __launch_bounds__(BLOCK) es_full(es_arguments a, Plan pl) {
+  using W = typename Ty<DT>::W;
+  __shared__ Shared<W> sh;
+  __shared__ Params sp;
+  const int64_t row = blockIdx.x;
+  const RowState st = *row_state(a, row);
+  if (st.part != PART_FULL) return;
+  block_params(a, row, &sp, sh);
+  const Params p = sp;
+  FullRow<DT, VEC> full(a, row, p, sh, pl.groups);
+  RowResult result = full.run(st.maximum, st.greedy, st.runner_up_id, st.valid);
+  result.target_status = ES_OK;
+  complete_row(a, row, p, result, st.fallbacks + full.fallbacks, st.route, sh);
+}
+
+}  // namespace es
+
+
+// ---------------------------------------------------------------------------
+// Per-dtype launchers, instantiated in one translation unit per dtype.
+namespace es {
+template <int DT, bool VEC, int G>
+hipError_t launch_main(const es_arguments& a, const Plan& pl, hipStream_t stream) {
+  const unsigned blocks = unsigned(pl.req_blocks + a.rows * pl.slices);
+  hipLaunchKernelGGL((es_main<DT, VEC, G>), dim3(blocks), dim3(BLOCK), 0, stream, a, pl);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || a.rows == 0) return err;
+  hipLaunchKernelGGL((es_full<DT, VEC>), dim3(unsigned(a.rows)), dim3(BLOCK), 0, stream, a, pl);
+  return hipGetLastError();
+}
+
+// Register tiles built for a dtype: the host picks one of them per call.
+template <int DT> struct Tiles;
+template <> struct Tiles<ES_F32> { static constexpr int n = 3; static constexpr int g[3] = {16, 8, 4}; };
+template <> struct Tiles<ES_BF16> { static constexpr int n = 3; static constexpr int g[3] = {16, 8, 4}; };
+template <> struct Tiles<ES_F16> { static constexpr int n = 1; static constexpr int g[3] = {4, 4, 4}; };
+template <> struct Tiles<ES_F64> { static constexpr int n = 1; static constexpr int g[3] = {4, 4, 4}; };
+
+// Contiguous rows aligned to a group of four use vector loads; any other
+// layout uses element loads with the smallest tile.
+template <int DT> hipError_t launch_dtype(const es_arguments& a, const Plan& pl, int g, bool vec, hipStream_t stream) {
+  if (!vec) return launch_main<DT, false, 4>(a, pl, stream);
+  if constexpr (Tiles<DT>::n == 3) {
+    if (g == 16) return launch_main<DT, true, 16>(a, pl, stream);
+    if (g == 8) return launch_main<DT, true, 8>(a, pl, stream);
+  }
+  return launch_main<DT, true, 4>(a, pl, stream);
+}
+}  // namespace es

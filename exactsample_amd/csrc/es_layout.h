@@ -1,0 +1,83 @@
+// Workspace layout of one call. Host and device agree on it; nothing outside
+// the library reads it except the FP64 recomputation counter (header word 1).
+//
+//   [0, 8)            header: int32 malformed-offsets flag, uint32 fallback count
+//   8 + r * ROW_BYTES row r's region (ROW_BYTES = 12320, the reference's
+//                     32 B RowResult + 12288 B scratch per row, api.h:37-43)
+//
+// A row's region sits at a fixed address whatever the call's row count, so the
+// arrival counters inside it stay where the previous call left them (zero):
+// every counter is reset by the block that completes it.
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+namespace es {
+
+constexpr size_t HEADER_BYTES = 8;
+constexpr size_t ROW_SCRATCH = 12288;
+constexpr size_t ROW_RESULT_BYTES = 32;
+constexpr size_t ROW_BYTES = ROW_RESULT_BYTES + ROW_SCRATCH;
+constexpr int MAX_SLICES = 64;
+
+// The outcome of one row, consumed by the request's finalize step.
+// p and q encode the ratio decision (p = 1 accepted, 0 rejected; q = 1), so
+// finalize's test u < min(1, p / q) reproduces it; sample is the substream-0
+// draw (bonus rows, coupled rows), residual the substream-2 draw after a rejection.
+struct RowResult {
+  double p, q;
+  int32_t sample, residual, status, target_status;
+};
+static_assert(sizeof(RowResult) == ROW_RESULT_BYTES, "RowResult is 32 bytes");
+
+// Which step finished a row in this call.
+enum Part : int32_t { PART_SKIP = 0, PART_DONE = 1, PART_FULL = 2 };
+
+// The merged statistics of a row (written by the block that merges it).
+struct RowState {
+  double maximum;       // largest valid logit
+  double runner_up;     // second valid logit in (value desc, id asc) order, -inf if none
+  int32_t greedy;       // lowest ID with the largest valid logit
+  int32_t runner_up_id; // INT_MAX if none
+  int32_t valid;        // allowed tokens with a logit above -inf
+  int32_t status;
+  int32_t part;
+  int32_t fallbacks;    // FP64 recomputations this row needed in this call
+  int32_t route;        // how the row was finished (diagnostics)
+  int32_t pad;
+};
+static_assert(sizeof(RowState) == 48, "RowState layout");
+
+// Arrival counters. slices: blocks of this row that finished the slice pass.
+// request: rows of the request completed (kept in the request's first row).
+// grid: rows completed in the call (kept in row 0).
+struct Counters {
+  uint32_t slices, request, grid, pad;
+};
+
+// One slice's summary of its part of the row.
+struct SlicePart {
+  double max_v;      // largest valid logit in the slice, -inf if none
+  double second_v;   // second in (value desc, id asc) order, -inf
+  double frontier;   // largest valid logit not stored as a candidate; -inf if none, +inf if unusable
+  double tau;        // candidates are the valid logits >= tau (-inf: all of them)
+  double sum;        // FP32 sum of exp((l - max_v) / T) over kept tokens, for top-p lists
+  double err;        // its error bound
+  int32_t max_id, second_id, valid, n_cand, pruned, flags;
+};
+static_assert(sizeof(SlicePart) == 72, "SlicePart layout");
+
+constexpr size_t OFF_RESULT = 0;
+constexpr size_t OFF_STATE = OFF_RESULT + ROW_RESULT_BYTES;
+constexpr size_t OFF_COUNTERS = OFF_STATE + sizeof(RowState);
+constexpr size_t OFF_PARTS = OFF_COUNTERS + sizeof(Counters);
+constexpr size_t OFF_CAND = OFF_PARTS + MAX_SLICES * sizeof(SlicePart);
+constexpr size_t CAND_BYTES = ROW_BYTES - OFF_CAND;
+static_assert(OFF_CAND % 16 == 0, "candidate area alignment");
+
+// A stored candidate: value and token ID.
+template <class W> struct Cand { W v; int32_t id; };
+template <> struct Cand<double> { double v; int32_t id, pad; };
+template <class W> constexpr int cand_capacity() { return int(CAND_BYTES / sizeof(Cand<W>)); }
+
+}  // namespace es

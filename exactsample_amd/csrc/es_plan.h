@@ -1,0 +1,27 @@
+// What the host decides per call and the per-dtype launchers it calls.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "exactsample_amd.h"
+
+namespace es {
+
+// Launch geometry chosen by the host for a call.
+struct Plan {
+  int32_t slices;        // blocks per row
+  int32_t groups;        // groups of 4 tokens per row
+  int32_t gps;           // groups per slice
+  int32_t req_blocks;    // request blocks at the front of the grid
+  int32_t cap_slice;     // candidates one slice may store
+  int32_t pad;
+};
+
+// Launches the kernel for logits of dtype DT with a register tile of g groups
+// of four per thread; vec selects vector loads (contiguous, aligned rows).
+template <int DT> hipError_t launch_dtype(const es_arguments& a, const Plan& pl, int g, bool vec, hipStream_t stream);
+extern template hipError_t launch_dtype<ES_F32>(const es_arguments&, const Plan&, int, bool, hipStream_t);
+extern template hipError_t launch_dtype<ES_BF16>(const es_arguments&, const Plan&, int, bool, hipStream_t);
+extern template hipError_t launch_dtype<ES_F16>(const es_arguments&, const Plan&, int, bool, hipStream_t);
+extern template hipError_t launch_dtype<ES_F64>(const es_arguments&, const Plan&, int, bool, hipStream_t);
+
+}  // namespace es

@@ -1,0 +1,106 @@
+/* exactsample_amd: C ABI of the MI355X (gfx950) sampling and draft-verification path.
+ *
+ * Drop-in boundary for the reference's C++ API (include/exactsample/api.h:7-44)
+ * and the op binding that fills it (csrc/bindings.cpp:45-136). Plain C types,
+ * plain pointers and sizes; no PyTorch types. A thin PyTorch op
+ * (exactsample_amd/csrc/binding.cpp) and a ctypes caller both sit on top.
+ *
+ * Semantics are the reference contract (docs/contract.md): per-request statuses,
+ * -1 tokens for failed requests, Philox keyed by (seed, stream, position,
+ * substream, token / 4) (docs/rng.md), ties split by token ID.
+ */
+#ifndef EXACTSAMPLE_AMD_H
+#define EXACTSAMPLE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Per-request status codes; replaces exactsample::Status (api.h:8). */
+enum es_status { ES_OK = 0, ES_NO_VALID_TOKEN = 1, ES_INVALID_INPUT = 2, ES_DRAFT_ZERO_PROB = 3 };
+/* path_used values; replaces exactsample::Path (api.h:9). */
+enum es_path { ES_PATH_REFERENCE = 0, ES_PATH_FUSED = 1 };
+/* Logit element types; replaces exactsample::DType (api.h:10). */
+enum es_dtype { ES_F32 = 0, ES_F64 = 1, ES_F16 = 2, ES_BF16 = 3 };
+/* Host-side error codes of es_launch (structural problems; numerical ones are statuses). */
+enum es_error {
+  ES_SUCCESS = 0,
+  ES_ERR_NULL_ARGUMENT = 1,     /* a required pointer is null */
+  ES_ERR_BAD_DIMENSION = 2,     /* rows/requests/vocab/max_draft out of the supported range */
+  ES_ERR_BAD_OPTION = 3,        /* mode, dispatch or list_max out of range */
+  ES_ERR_WORKSPACE_SIZE = 4,    /* workspace smaller than es_workspace_size() */
+  ES_ERR_WORKSPACE_ALIGN = 5,   /* workspace not 8-byte aligned */
+  ES_ERR_BAD_DTYPE = 6,         /* unknown es_dtype, or draft dtype differs from target */
+  ES_ERR_LAUNCH = 7             /* the HIP runtime refused a kernel launch */
+};
+
+/* A [rows, vocab] logits matrix with element strides; replaces exactsample::Matrix (api.h:11-15). */
+typedef struct es_matrix {
+  const void* data;
+  int64_t s0, s1;
+  int32_t dtype; /* enum es_dtype */
+  int32_t pad;
+} es_matrix;
+
+/* A strided vector; replaces exactsample::Vector<T> (api.h:16-19). */
+typedef struct es_vec_i64 { const int64_t* data; int64_t stride; } es_vec_i64;
+typedef struct es_vec_f64 { const double* data; int64_t stride; } es_vec_f64;
+
+/* Everything one call needs; replaces exactsample::Arguments (api.h:21-36).
+ * All pointers are device pointers. Strides are in elements. */
+typedef struct es_arguments {
+  es_matrix target;        /* [rows, vocab] */
+  es_matrix draft;         /* full-q draft logits, same shape and dtype, or data == NULL */
+  es_vec_i64 cu_rows;      /* [requests + 1] */
+  es_vec_i64 top_k;        /* [requests], 0 disables */
+  es_vec_i64 draft_kind;   /* [requests], 0 one-hot, 1 full */
+  es_vec_i64 seed;         /* [requests], signed storage of the uint64 key */
+  es_vec_i64 stream;       /* [requests], in [0, 2^32) */
+  es_vec_i64 position;     /* [rows], in [0, 2^32) */
+  es_vec_f64 temperature;  /* [requests] */
+  es_vec_f64 top_p;        /* [requests] */
+  es_vec_f64 min_p;        /* [requests] */
+  const int64_t* draft_ids; int64_t draft_s0, draft_s1;  /* [requests, >= max_draft] */
+  const int32_t* mask; int64_t mask_s0, mask_s1;         /* [rows, ceil(vocab/32)] or NULL */
+  int64_t* tokens; int64_t token_s0, token_s1;           /* [>= requests, >= max_draft + 1] */
+  int32_t* accepted; int64_t accepted_s;                 /* [>= requests] */
+  int32_t* status; int64_t status_s;                     /* [>= requests] */
+  int32_t* path; int64_t path_s;                         /* [>= requests] */
+  int64_t rows, requests, vocab, max_draft;
+  int32_t mode;            /* 0 ratio, 1 coupled */
+  int32_t dispatch;        /* 0 auto, 1 reference, 2 fused */
+  int32_t list_max;        /* largest kept set finished as an FP64 list, 0..256 */
+  int32_t pad;
+  uint8_t* workspace;      /* es_workspace_size() bytes, zeroed once when allocated */
+  uint64_t workspace_bytes;
+} es_arguments;
+
+/* Bytes of workspace for `rows` rows; `reference` != 0 adds the dispatch="reference"
+ * scratch. Same formula as exactsample::workspace_size (api.h:37-43):
+ * 8 + rows * (32 + max(12288, reference ? 20 * vocab : 0)). Returns 0 on overflow. */
+size_t es_workspace_size(int64_t rows, int64_t vocab, int32_t reference);
+
+/* Enqueues one call on `stream` (a hipStream_t; NULL is the null stream). Never
+ * allocates, never synchronizes. Replaces exactsample::launch (api.h:44,
+ * csrc/verify/verify.cu:220-228). Returns an es_error code. */
+int32_t es_launch(const es_arguments* args, void* stream);
+
+/* A static description of an es_error code. */
+const char* es_error_string(int32_t code);
+
+/* The last HIP runtime error string seen by es_launch on this thread ("" if none). */
+const char* es_last_hip_error(void);
+
+/* Offset of the FP64 recomputation counter in the workspace (a uint32 written by
+ * each call; read it after the call completes). Replaces workspace word 1 read at
+ * python/exactsample/cuda.py:109-114. */
+size_t es_fallback_counter_offset(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EXACTSAMPLE_AMD_H */
