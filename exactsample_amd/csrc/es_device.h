@@ -26,18 +26,63 @@ __device__ __forceinline__ uint64_t xshfl(uint64_t v, int m) {
   return (uint64_t(__shfl_xor(unsigned(v >> 32), m, WAVE)) << 32) | __shfl_xor(unsigned(v), m, WAVE);
 }
 
-// op over all 64 lanes; every lane receives bitwise the same value because
-// each butterfly step combines the same two operands on both partners.
-template <class T, class Op> __device__ __forceinline__ T wave_all(T v, Op op) {
+// ---------------------------------------------------------------------------
+// Wave scans and reductions on DPP lane moves. A __shfl lowers to
+// ds_bpermute, an LDS round trip per step; the DPP row shifts and row
+// broadcasts below cost a few cycles each. They need every lane of the wave
+// active (all callers run them in wave-uniform control flow).
+constexpr int DPP_ROW_SHR1 = 0x111, DPP_ROW_SHR2 = 0x112, DPP_ROW_SHR4 = 0x114, DPP_ROW_SHR8 = 0x118;
+constexpr int DPP_ROW_BCAST15 = 0x142, DPP_ROW_BCAST31 = 0x143;
+
+// Lane i receives x from its DPP source lane; lanes whose source lies outside
+// their row, or whose row is not in ROWS, receive `fill`.
+template <int CTRL, int ROWS, class T> __device__ __forceinline__ T dpp_move(T x, T fill) {
+  static_assert(sizeof(T) % 4 == 0, "32-bit words");
+  constexpr int N = int(sizeof(T) / 4);
+  int a[N], f[N];
+  __builtin_memcpy(a, &x, sizeof(T));
+  __builtin_memcpy(f, &fill, sizeof(T));
 #pragma unroll
-  for (int m = WAVE / 2; m; m >>= 1) v = op(v, xshfl(v, m));
-  return v;
+  for (int k = 0; k < N; ++k) a[k] = __builtin_amdgcn_update_dpp(f[k], a[k], CTRL, ROWS, 0xF, false);
+  T r;
+  __builtin_memcpy(&r, a, sizeof(T));
+  return r;
+}
+
+// The value of lane `src` (wave-uniform) in every lane.
+template <class T> __device__ __forceinline__ T lane_read(T x, int src) {
+  static_assert(sizeof(T) % 4 == 0, "32-bit words");
+  constexpr int N = int(sizeof(T) / 4);
+  int a[N];
+  __builtin_memcpy(a, &x, sizeof(T));
+#pragma unroll
+  for (int k = 0; k < N; ++k) a[k] = __builtin_amdgcn_readlane(a[k], src);
+  T r;
+  __builtin_memcpy(&r, a, sizeof(T));
+  return r;
+}
+
+// Inclusive scan in lane order: lane i gets op(... op(op(x0, x1), x2) ..., xi)
+// up to the grouping of the steps. `identity` must satisfy op(identity, x) == x.
+template <class T, class Op> __device__ __forceinline__ T wave_scan(T x, Op op, T identity) {
+  x = op(dpp_move<DPP_ROW_SHR1, 0xF>(x, identity), x);
+  x = op(dpp_move<DPP_ROW_SHR2, 0xF>(x, identity), x);
+  x = op(dpp_move<DPP_ROW_SHR4, 0xF>(x, identity), x);
+  x = op(dpp_move<DPP_ROW_SHR8, 0xF>(x, identity), x);
+  x = op(dpp_move<DPP_ROW_BCAST15, 0xA>(x, identity), x);  // rows 1 and 3 take the row before's last lane
+  x = op(dpp_move<DPP_ROW_BCAST31, 0xC>(x, identity), x);  // rows 2 and 3 take lane 31
+  return x;
+}
+
+// op over all 64 lanes, the same value in every lane (lane 63's scan).
+template <class T, class Op> __device__ __forceinline__ T wave_all(T v, Op op, T identity) {
+  return lane_read(wave_scan(v, op, identity), WAVE - 1);
 }
 
 // op over the block, combined across waves in wave order; every thread gets it.
 // `scratch` holds WAVES entries and may be reused right after the call.
-template <class T, class Op> __device__ __forceinline__ T block_all(T v, Op op, T* scratch) {
-  v = wave_all(v, op);
+template <class T, class Op> __device__ __forceinline__ T block_all(T v, Op op, T* scratch, T identity) {
+  v = wave_all(v, op, identity);
   __syncthreads();
   if (lane_id() == 0) scratch[wave_id()] = v;
   __syncthreads();
@@ -49,13 +94,19 @@ template <class T, class Op> __device__ __forceinline__ T block_all(T v, Op op, 
 
 // Inclusive prefix sum over the wave in lane order.
 template <class T> __device__ __forceinline__ T wave_scan_add(T v) {
-  const int l = lane_id();
+  return wave_scan(v, [](T x, T y) { return x + y; }, T(0));
+}
+
+// The j-th largest (1-based) of the wave's 64 unsigned keys, by a bitwise
+// search on ballots (no cross-lane data movement).
+template <class K> __device__ __forceinline__ K wave_kth_largest(K key, int j) {
+  K prefix = 0;
 #pragma unroll
-  for (int o = 1; o < WAVE; o <<= 1) {
-    T y = __shfl_up(v, o, WAVE);
-    if (l >= o) v += y;
+  for (int b = int(sizeof(K) * 8) - 1; b >= 0; --b) {
+    const K cand = prefix | (K(1) << b);
+    if (__popcll(__ballot(key >= cand)) >= j) prefix = cand;
   }
-  return v;
+  return prefix;
 }
 
 // Inclusive prefix sum over the block in thread order; *total receives the sum.

@@ -279,6 +279,16 @@ template <class W> struct Shared {
   int32_t status;
   int pick;
   unsigned __int128 ck;
+  // Slice-block lookup and statistics, one entry per wave (never reused).
+  int lk_bad[WAVES], lk_found[WAVES];
+  int64_t lk_begin[WAVES], lk_end[WAVES];
+  W st_max[WAVES], st_thr[WAVES];
+  int st_id[WAVES], st_valid[WAVES], st_bad[WAVES];
+  int appended;
+  int meta_bad;
+  // The merge wave's decision, broadcast to the block.
+  RowResult wres;
+  int wroute, wfallbacks, wdone;
 };
 
 // The request's parameters, read once per block.
@@ -358,6 +368,98 @@ __device__ __forceinline__ void block_params(const es_arguments& a, int64_t row,
   __syncthreads();
 }
 
+// The owner lookup and scalar parameters of a slice block. x0 and x1 are
+// cu_rows[tid] and cu_rows[tid + 1] (valid for tid < requests), loaded before
+// the logit tile: waits for them then leave the tile loads in flight. Longer
+// offset vectors are scanned in further chunks here. The request's scalar
+// parameters are checked (reference verify.cu:6-40); the per-row positions and
+// draft IDs are checked by the block that merges the row (request_rows_ok).
+template <class SH>
+__device__ __forceinline__ void slice_lookup(const es_arguments& a, int64_t row, int64_t x0, int64_t x1, Params* p,
+                                             SH& sh) {
+  const int tid = threadIdx.x;
+  const int64_t R = a.requests;
+  int bad = 0, found = -1;
+  int64_t fb = 0, fe = 0;
+  auto visit = [&](int64_t i, int64_t x, int64_t y) {
+    bad |= x < 0 || y > a.rows || x > y || (i == 0 && x != 0) || (i == R - 1 && y != a.rows);
+    if (x <= row && row < y) { found = int(i); fb = x; fe = y; }
+  };
+  if (tid < R) visit(tid, x0, x1);
+  for (int64_t i = tid + BLOCK; i < R; i += BLOCK) visit(i, at(a.cu_rows, i), at(a.cu_rows, i + 1));
+  const uint64_t any_found = __ballot(found >= 0);
+  const int src = any_found ? __ffsll((unsigned long long)any_found) - 1 : 0;
+  const int wfound = any_found ? lane_read(found, src) : -1;
+  const int64_t wb = lane_read(fb, src), we = lane_read(fe, src);
+  const int wbad = __ballot(bad) != 0;
+  if (lane_id() == 0) {
+    sh.lk_bad[wave_id()] = wbad;
+    sh.lk_found[wave_id()] = wfound;
+    sh.lk_begin[wave_id()] = wb;
+    sh.lk_end[wave_id()] = we;
+  }
+  __syncthreads();
+  int malformed = 0, req = -1;
+  int64_t begin = 0, end = 0;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) {
+    malformed |= sh.lk_bad[w];
+    if (req < 0 && sh.lk_found[w] >= 0) { req = sh.lk_found[w]; begin = sh.lk_begin[w]; end = sh.lk_end[w]; }
+  }
+  req = __builtin_amdgcn_readfirstlane(req);
+  p->status = ES_OK;
+  if (malformed || req < 0 || end - begin > a.max_draft + 1) {
+    p->status = ES_INVALID_INPUT;
+    return;
+  }
+  const double t = at(a.temperature, req), pp = at(a.top_p, req), m = at(a.min_p, req);
+  const int64_t k = at(a.top_k, req), kind = at(a.draft_kind, req), stream = at(a.stream, req);
+  const bool scalar_bad = !isfinite(t) || t < 0 || !isfinite(pp) || pp <= 0 || pp > 1 || !isfinite(m) || m < 0 ||
+                          m > 1 || k < 0 || k > a.vocab || kind < 0 || kind > 1 || (a.mode == 1 && kind == 1) ||
+                          (kind == 1 && end - begin > 1 && !a.draft.data) || stream < 0 ||
+                          uint64_t(stream) > 0xffffffffull;
+  if (scalar_bad) {
+    p->status = ES_INVALID_INPUT;
+    return;
+  }
+  p->req = req;
+  p->begin = begin;
+  p->end = end;
+  p->temperature = t;
+  p->top_p = pp;
+  p->min_p = m;
+  p->top_k = k;
+  p->draft_row = row + 1 < end;
+  p->coupled = a.mode == 1;
+  p->verify = p->draft_row && !p->coupled;
+  p->full_q = p->draft_row && kind == 1;
+  p->draft_id = -1;
+  p->rng.stream = uint32_t(stream);
+}
+
+// The per-row metadata of a request (positions and draft IDs in range),
+// checked by one wave.
+__device__ __forceinline__ bool request_rows_ok(const es_arguments& a, const Params& p) {
+  int bad = 0;
+  for (int64_t r = p.begin + lane_id(); r < p.end; r += WAVE) {
+    const int64_t pos = at(a.position, r);
+    bad |= pos < 0 || uint64_t(pos) > 0xffffffffull;
+    if (r + 1 < p.end) {
+      const int64_t id = draft_at(a, p.req, r - p.begin);
+      bad |= id < 0 || id >= a.vocab;
+    }
+  }
+  return __ballot(bad) == 0;
+}
+
+// The row's RNG address and draft ID (range-checked by request_rows_ok
+// before any use that depends on the range).
+__device__ __forceinline__ void load_row_rng(const es_arguments& a, int64_t row, Params* p) {
+  p->rng.seed = uint64_t(at(a.seed, p->req));
+  p->rng.position = uint32_t(at(a.position, row));
+  p->draft_id = p->draft_row ? int(draft_at(a, p->req, row - p->begin)) : -1;
+}
+
 // ---------------------------------------------------------------------------
 // The commit of one request from its rows' results (reference verify.cu:169-217),
 // run by one wave. Lane l takes rows begin + l, begin + l + 64, ...
@@ -375,7 +477,7 @@ __device__ __forceinline__ void finalize_request(const es_arguments& a, int64_t 
       }
       const uint64_t bad = __ballot(s != ES_OK);
       if (bad) {
-        const int first = __shfl(s, __ffsll((unsigned long long)bad) - 1, WAVE);
+        const int first = lane_read(s, __ffsll((unsigned long long)bad) - 1);
         for (int64_t i = lane; i <= a.max_draft; i += WAVE) tokens[i * a.token_s1] = -1;
         if (lane == 0) {
           a.accepted[req * a.accepted_s] = 0;
@@ -427,7 +529,7 @@ template <class W> __device__ __forceinline__ void grid_arrive(const es_argument
   if (arrive(&counters(a, 0)->grid, uint32_t(a.rows), &sh.flag)) {
     unsigned total = 0;
     for (int64_t r = threadIdx.x; r < a.rows; r += BLOCK) total += unsigned(ld_dev32(&row_state(a, r)->fallbacks));
-    total = block_all(total, [](unsigned x, unsigned y) { return x + y; }, reinterpret_cast<unsigned*>(sh.ired));
+    total = block_all(total, [](unsigned x, unsigned y) { return x + y; }, reinterpret_cast<unsigned*>(sh.ired), 0u);
     if (threadIdx.x == 0) reinterpret_cast<uint32_t*>(a.workspace)[1] = total;
   }
 }
@@ -550,11 +652,7 @@ __device__ __forceinline__ int list_draw(const Params& p, Shared<W>& sh, int n, 
   struct SI { double s; int id; };
   SI v{best, best_id};
   auto op = [](SI x, SI y) { return (y.s > x.s || (y.s == x.s && y.id < x.id)) ? y : x; };
-#pragma unroll
-  for (int m = WAVE / 2; m; m >>= 1) {
-    SI o{xshfl(v.s, m), xshfl(v.id, m)};
-    v = op(v, o);
-  }
+  v = wave_all(v, op, SI{-INFINITY, INT_MAX});
   __syncthreads();
   if (lane_id() == 0) { sh.dred[wave_id()] = v.s; sh.ired[wave_id()] = v.id; }
   __syncthreads();
@@ -566,11 +664,12 @@ __device__ __forceinline__ int list_draw(const Params& p, Shared<W>& sh, int n, 
 
 // DD sum over the block in thread order (deterministic for a fixed block shape).
 template <class W> __device__ __forceinline__ DD block_dd(DD v, Shared<W>& sh) {
-  return block_all(v, [](DD x, DD y) { return dd_add(x, y); }, sh.ddred);
+  return block_all(v, [](DD x, DD y) { return dd_add(x, y); }, sh.ddred, DD{0, 0});
 }
 
-// The correctly rounded sum of sh.u.list.w[0, n): certified DD, else exact.
-template <class W> __device__ __forceinline__ double list_fsum(Shared<W>& sh, int n, int* fallbacks) {
+// The correctly rounded sum of sh.u.list.w[0, n): certified DD, else exact
+// (an exact sum on a rounding tie is part of the FP64 path, not a fallback).
+template <class W> __device__ __forceinline__ double list_fsum(Shared<W>& sh, int n) {
   DD acc{0, 0};
   for (int i = threadIdx.x; i < n; i += BLOCK) acc = dd_add(acc, DD{sh.u.list.w[i], 0});
   acc = block_dd(acc, sh);
@@ -580,7 +679,7 @@ template <class W> __device__ __forceinline__ double list_fsum(Shared<W>& sh, in
   __syncthreads();
   for (int i = threadIdx.x; i < n; i += BLOCK) sacc_add(sh.limbs, sh.u.list.w[i]);
   __syncthreads();
-  if (threadIdx.x == 0) { sh.dred[0] = sacc_round(sh.limbs); ++*fallbacks; }
+  if (threadIdx.x == 0) sh.dred[0] = sacc_round(sh.limbs);
   __syncthreads();
   r = sh.dred[0];
   __syncthreads();
@@ -691,14 +790,14 @@ __device__ __forceinline__ bool list_finish(const es_arguments& a, int64_t row, 
     sh.u.list.w[i] = w;
     if (!(w >= p.min_p && w > 0.0)) first_out = min(first_out, i);
   }
-  first_out = block_all(first_out, [](int x, int y) { return x < y ? x : y; }, sh.ired);
+  first_out = block_all(first_out, [](int x, int y) { return x < y ? x : y; }, sh.ired, INT_MAX);
   const int n1 = min(n_out, first_out);
   int n2 = n1;
   if (p.top_p < 1) {
     double lo_t, hi_t;
     const bool whole = topk_mode || (whole_union && n_u == sh.valid);  // the list is the whole kept set
     if (whole) {
-      const double total = list_fsum(sh, n1, fallbacks);
+      const double total = list_fsum(sh, n1);
       lo_t = hi_t = p.top_p * total;
     } else {
       if (!(sh.err >= 0) || !(sh.sum - sh.err > 0)) { *why = 4; return false; }
@@ -713,13 +812,8 @@ __device__ __forceinline__ bool list_finish(const es_arguments& a, int64_t row, 
       if (i < n1) local = dd_add(local, DD{sh.u.list.w[i], 0});
     }
     // Exclusive scan of the per-thread sums in thread order.
-    DD incl = local;
+    const DD incl = wave_scan(local, [](DD x, DD y) { return dd_add(x, y); }, DD{0, 0});
     const int lane = lane_id();
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-      const DD y{__shfl_up(incl.hi, o, WAVE), __shfl_up(incl.lo, o, WAVE)};
-      if (lane >= o) incl = dd_add(y, incl);
-    }
     __syncthreads();
     if (lane == WAVE - 1) sh.ddred[wave_id()] = incl;
     __syncthreads();
@@ -739,9 +833,9 @@ __device__ __forceinline__ bool list_finish(const es_arguments& a, int64_t row, 
       if (rl < 0 || rh < 0) unsure = min(unsure, i);
     }
     auto mn = [](int x, int y) { return x < y ? x : y; };
-    first_lo = block_all(first_lo, mn, sh.ired);
-    first_hi = block_all(first_hi, mn, sh.ired);
-    unsure = block_all(unsure, mn, sh.ired);
+    first_lo = block_all(first_lo, mn, sh.ired, INT_MAX);
+    first_hi = block_all(first_hi, mn, sh.ired, INT_MAX);
+    unsure = block_all(unsure, mn, sh.ired, INT_MAX);
     if (unsure <= first_hi || first_lo != first_hi) { *why = 5; return false; }
     if (first_hi == INT_MAX) {
       if (!whole) { *why = 6; return false; }  // the nucleus may extend past the list
@@ -750,7 +844,7 @@ __device__ __forceinline__ bool list_finish(const es_arguments& a, int64_t row, 
       n2 = first_hi + 1;
     }
   }
-  const double den = list_fsum(sh, n2, fallbacks);
+  const double den = list_fsum(sh, n2);
   for (int i = threadIdx.x; i < n2; i += BLOCK) sh.u.list.w[i] = sh.u.list.w[i] / den;
   __syncthreads();
   RowResult r{0, 1, -1, -1, ES_OK, ES_OK};
@@ -758,7 +852,7 @@ __device__ __forceinline__ bool list_finish(const es_arguments& a, int64_t row, 
     int at_draft = INT_MAX;
     for (int i = threadIdx.x; i < n2; i += BLOCK)
       if (sh.u.list.sid[i] == p.draft_id) at_draft = i;
-    at_draft = block_all(at_draft, [](int x, int y) { return x < y ? x : y; }, sh.ired);
+    at_draft = block_all(at_draft, [](int x, int y) { return x < y ? x : y; }, sh.ired, INT_MAX);
     const double px = at_draft == INT_MAX ? 0.0 : sh.u.list.w[at_draft];
     const double u = uniform64(word_of(p.rng, 1u, 0u));
     const bool accept = u < fmin(1.0, px);
@@ -769,6 +863,180 @@ __device__ __forceinline__ bool list_finish(const es_arguments& a, int64_t row, 
   }
   *result = r;
   return true;
+}
+
+// ---------------------------------------------------------------------------
+// Top-k rows (k <= 64) finished by one wave from the slices' sorted lists.
+//
+// Every slice stored its first min(k, valid) tokens in (value desc, ID asc)
+// order; the last of them is its frontier (none when it stored every valid
+// token). The union is complete down to the earliest frontier F, and the
+// slice owning F stored k tokens up to it, so the row's first k tokens are in
+// the union at or before F. Among those entries a bitwise search on ballots
+// finds the k-th largest value T; the pool (the entries >= T: the first k
+// plus any ties at T) is rank-sorted and the FP64 finish follows the oracle
+// (reference.py:60-104): weights exp((l - max) / T), the min-p/positivity
+// cut, the top-k prefix, the shortest top-p prefix by certified double-double
+// prefix sums, the correctly rounded denominator and the Gumbel-argmax draw.
+//
+// Returns 1 with *out set, 0 when the union or the pool does not fit (the
+// block list takes the row) and -1 when a rounding could not be certified
+// (the full-row path recomputes it exactly).
+constexpr int WAVE_BATCH = 8;      // candidate slots per lane fetched together
+constexpr int UNION_PER_LANE = 8;  // union entries per lane the wave selects from
+
+// The position of each lane's (v, id) among the first n lanes' entries in
+// (value desc, ID asc) order; entries are distinct. Lane values are read with
+// readlane (no LDS round trips).
+template <class W> __device__ __forceinline__ int wave_rank(W v, int id, int n) {
+  int rank = 0;
+  for (int j = 0; j < n; ++j) rank += before(lane_read(v, j), lane_read(id, j), v, id);
+  return rank;
+}
+
+template <class W>
+__device__ __forceinline__ int wave_topk(const es_arguments& a, int64_t row, const Params& p, Shared<W>& sh,
+                                         const Cand<W> (&pre)[WAVE_BATCH], int slices, int cap, int k, double M,
+                                         double F, int F_id, int valid_all, RowResult* out) {
+  using K = typename std::conditional<sizeof(W) == 8, uint64_t, uint32_t>::type;
+  const int lane = lane_id();
+  const int slots = slices * k;
+  if (slots > WAVE * WAVE_BATCH) return 0;
+  // The slice of a slot (idx / k without a division: idx < 2^12, k <= 64, so
+  // the 20-bit reciprocal is exact).
+  const uint32_t inv_k = ((1u << 20) + uint32_t(k) - 1) / uint32_t(k);
+  // The union at or before F, compacted into LDS in slot order.
+  int n_u = 0;
+#pragma unroll
+  for (int r = 0; r < WAVE_BATCH; ++r) {
+    const int idx = lane + WAVE * r;
+    const int sl = int((uint64_t(uint32_t(idx)) * inv_k) >> 20);
+    const double d = double(pre[r].v);
+    const bool take = idx < slots && idx - sl * k < sh.n_cand[min(sl, MAX_SLICES - 1)] &&
+                      (d > F || (d == F && pre[r].id <= F_id));
+    const uint64_t mk = __ballot(take);
+    const int pos = n_u + __popcll(mk & ((1ull << lane) - 1ull));
+    if (take && pos < WAVE * UNION_PER_LANE) { sh.u.list.v[pos] = pre[r].v; sh.u.list.id[pos] = pre[r].id; }
+    n_u += __popcll(mk);
+  }
+  const int n_keep = p.top_k > 0 && p.top_k < valid_all ? int(p.top_k) : valid_all;
+  if (n_u > WAVE * UNION_PER_LANE) return 0;
+  if (n_u < n_keep || n_keep < 1) return -1;  // cannot happen for a complete union
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  // The n_keep-th largest value of the union: its order key, bit by bit.
+  const int per = (n_u + WAVE - 1) / WAVE;
+  K key[UNION_PER_LANE];
+#pragma unroll
+  for (int r = 0; r < UNION_PER_LANE; ++r) {
+    const int idx = lane + WAVE * r;
+    key[r] = r < per && idx < n_u ? order_key(sh.u.list.v[idx]) : K(0);
+  }
+  K prefix = 0;
+  for (int b = int(sizeof(K) * 8) - 1; b >= 0; --b) {
+    const K cand = prefix | (K(1) << b);
+    int count = 0;
+#pragma unroll
+    for (int r = 0; r < UNION_PER_LANE; ++r)
+      if (r < per) count += __popcll(__ballot(key[r] >= cand));
+    if (count >= n_keep) prefix = cand;
+  }
+  // The pool: union entries >= that value, one per lane.
+  int n_pool = 0;
+#pragma unroll
+  for (int r = 0; r < UNION_PER_LANE; ++r) {
+    if (r >= per) break;
+    const int idx = lane + WAVE * r;
+    const bool take = idx < n_u && key[r] >= prefix;
+    const uint64_t mk = __ballot(take);
+    const int pos = n_pool + __popcll(mk & ((1ull << lane) - 1ull));
+    if (take && pos < WAVE) { sh.u.list.sv[pos] = sh.u.list.v[idx]; sh.u.list.sid[pos] = sh.u.list.id[idx]; }
+    n_pool += __popcll(mk);
+  }
+  if (n_pool > WAVE) return 0;  // a wide tie at the k-th value
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  // Rank sort of the pool, one entry per lane.
+  W v = neg_inf<W>();
+  int id = INT_MAX;
+  if (lane < n_pool) { v = sh.u.list.sv[lane]; id = sh.u.list.sid[lane]; }
+  const int rank = wave_rank(v, id, n_pool);
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  if (lane < n_pool) { sh.u.list.v[rank] = v; sh.u.list.id[rank] = id; }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  if (lane < n_pool) { v = sh.u.list.v[lane]; id = sh.u.list.id[lane]; }
+  // Weights and the min-p/positivity cut (a suffix of the order).
+  const double T = p.temperature;
+  const bool in_k = lane < n_keep;
+  const double w = in_k ? exp((double(v) - M) / T) : 0.0;
+  const uint64_t out_mask = __ballot(in_k && !(w >= p.min_p && w > 0.0));
+  const int n1 = out_mask ? min(n_keep, __ffsll((unsigned long long)out_mask) - 1) : n_keep;
+  const double wk = lane < n1 ? w : 0.0;
+  // Inclusive double-double prefix sums in lane order, each with its bound.
+  const DD incl = wave_scan(DD{wk, 0}, [](DD x, DD y) { return dd_add(x, y); }, DD{0, 0});
+  const double err = dd_sum_error(incl, lane + 1) + 4 * 0x1p-104 * incl.hi;
+  // The correctly rounded sum of the first n weights (math.fsum): certified
+  // from the double-double prefix, or, when the exact sum may sit on a
+  // rounding tie (sums of two or three bf16-derived weights often do),
+  // computed exactly with the LDS superaccumulator.
+  auto rounded_prefix = [&](int n) {
+    const DD s = lane_read(incl, n - 1);
+    double r;
+    if (dd_round_certain(s, dd_sum_error(s, n) + 4 * 0x1p-104 * s.hi, &r)) return r;
+    if (lane < SACC_LIMBS) sh.limbs[lane] = 0;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    if (lane < n) sacc_add(sh.limbs, wk);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    r = 0;
+    if (lane == 0) r = sacc_round(sh.limbs);
+    return lane_read(r, 0);
+  };
+  if (n1 == 0) return -1;  // the maximum always survives; defensive
+  double den = rounded_prefix(n1);
+  int count = n1;
+  if (p.top_p < 1) {
+    // The shortest prefix whose rounded sum reaches top_p * den
+    // (reference.py:76-83): certain lanes from the double-double bounds, the
+    // uncertain ones before the first certain hit decided exactly, in order.
+    const double target = p.top_p * den;
+    const int reach = lane < n1 ? dd_reaches(incl, err, target) : 0;
+    const uint64_t yes = __ballot(reach == 1);
+    const int first_yes = yes ? __ffsll((unsigned long long)yes) - 1 : n1;
+    uint64_t unsure = __ballot(reach < 0) & (first_yes < WAVE ? (1ull << first_yes) - 1ull : ~0ull);
+    count = yes ? first_yes + 1 : n1;
+    while (unsure) {
+      const int j = __ffsll((unsigned long long)unsure) - 1;
+      unsure &= unsure - 1;
+      if (rounded_prefix(j + 1) >= target) { count = j + 1; break; }
+    }
+    if (count != n1) den = rounded_prefix(count);
+  }
+  const bool kept = lane < count;
+  const double pr = kept ? wk / den : 0.0;
+  // Gumbel-argmax over kept tokens with positive probability, lowest ID on ties.
+  auto draw = [&](uint32_t sub, int excluded) {
+    double s = -INFINITY;
+    int sid = INT_MAX;
+    if (kept && pr > 0 && id != excluded) {
+      s = log(pr) + gumbel64(word_of(p.rng, sub, uint32_t(id)));
+      sid = id;
+    }
+    struct SI { double s; int id; };
+    const SI best = wave_all(SI{s, sid}, [](SI x, SI y) { return (y.s > x.s || (y.s == x.s && y.id < x.id)) ? y : x; },
+                             SI{-INFINITY, INT_MAX});
+    return best.id == INT_MAX ? -1 : best.id;
+  };
+  RowResult r{0, 1, -1, -1, ES_OK, ES_OK};
+  if (p.verify) {
+    const uint64_t at = __ballot(kept && id == p.draft_id);
+    const double px = at ? lane_read(pr, __ffsll((unsigned long long)at) - 1) : 0.0;
+    const double u = uniform64(word_of(p.rng, 1u, 0u));
+    const bool accept = u < fmin(1.0, px);
+    r.p = accept ? 1.0 : 0.0;
+    if (!accept) r.residual = draw(2u, p.draft_id);
+  } else {
+    r.sample = draw(0u, -1);
+  }
+  *out = r;
+  return 1;
 }
 
 // ---------------------------------------------------------------------------
@@ -823,7 +1091,7 @@ template <int DT, bool VEC> struct FullRow {
 
   // The correctly rounded sum of f(t, v) over tokens (f returns a weight >= 0,
   // or 0 to skip); certified DD first, exact superaccumulator otherwise.
-  template <bool Q, class F> __device__ double exact_sum(F&& f, bool count_fallback) {
+  template <bool Q, class F> __device__ __forceinline__ double exact_sum(F&& f, bool count_fallback) {
     if (count_fallback) ++fallbacks;
     DD acc{0, 0};
     int n = 0;
@@ -832,7 +1100,7 @@ template <int DT, bool VEC> struct FullRow {
       if (w > 0) { acc = dd_add(acc, DD{w, 0}); ++n; }
     });
     acc = block_dd(acc, sh);
-    n = block_all(n, [](int x, int y) { return x + y; }, sh.ired);
+    n = block_all(n, [](int x, int y) { return x + y; }, sh.ired, 0);
     double r;
     if (dd_round_certain(acc, dd_sum_error(acc, n), &r)) return r;
     sacc_clear(sh.limbs);
@@ -851,7 +1119,7 @@ template <int DT, bool VEC> struct FullRow {
 
   // The n-th (1-based) composite key, in descending order, among tokens where
   // pred(t, v, ok) holds: radix selection over 11-bit digits of the composite.
-  template <class Pred> __device__ u128 select_nth(int n, Pred&& pred) {
+  template <class Pred> __device__ __forceinline__ u128 select_nth(int n, Pred&& pred) {
     constexpr int NB = CK<W>::BITS;
     constexpr int D = 11;
     u128 prefix = 0;
@@ -908,7 +1176,7 @@ template <int DT, bool VEC> struct FullRow {
 
   // The first composite key (descending order) among tokens where pred holds at
   // which the correctly rounded running sum of weight(t, v) reaches target.
-  template <class Pred, class Wt> __device__ u128 mass_boundary(double target, Pred&& pred, Wt&& weight) {
+  template <class Pred, class Wt> __device__ __forceinline__ u128 mass_boundary(double target, Pred&& pred, Wt&& weight) {
     constexpr int NB = CK<W>::BITS;
     constexpr int D = 11;
     u128 prefix = 0;
@@ -940,13 +1208,10 @@ template <int DT, bool VEC> struct FullRow {
         local_err += double(sh.u.hist.cnt[d]) * 0x1p-52 * m;
       }
       // Exclusive prefix over threads (FP64, fixed order) with a generous bound.
-      double incl = local, incl_e = local_err;
+      struct ME { double m, e; };
+      const ME sc = wave_scan(ME{local, local_err}, [](ME x, ME y) { return ME{x.m + y.m, x.e + y.e}; }, ME{0, 0});
+      const double incl = sc.m, incl_e = sc.e;
       const int lane = lane_id();
-#pragma unroll
-      for (int o = 1; o < WAVE; o <<= 1) {
-        const double y = __shfl_up(incl, o, WAVE), ye = __shfl_up(incl_e, o, WAVE);
-        if (lane >= o) { incl += y; incl_e += ye; }
-      }
       __syncthreads();
       if (lane == WAVE - 1) { sh.dred[wave_id()] = incl; reinterpret_cast<double*>(sh.ddred)[wave_id()] = incl_e; }
       __syncthreads();
@@ -969,8 +1234,8 @@ template <int DT, bool VEC> struct FullRow {
         if (lo >= target) first_sure = min(first_sure, rank);
       }
       auto mn = [](int x, int y) { return x < y ? x : y; };
-      first = block_all(first, mn, sh.ired);
-      first_sure = block_all(first_sure, mn, sh.ired);
+      first = block_all(first, mn, sh.ired, INT_MAX);
+      first_sure = block_all(first_sure, mn, sh.ired, INT_MAX);
       if (first == INT_MAX) {
         // Rounding never reaches the target inside this region: take its last token.
         first = first_sure = INT_MAX - 1;
@@ -982,7 +1247,7 @@ template <int DT, bool VEC> struct FullRow {
           int last = -1;
           for (int d = threadIdx.x; d < buckets; d += BLOCK)
             if (sh.u.hist.cnt[d]) last = max(last, buckets - 1 - d);
-          last = block_all(last, [](int x, int y) { return x > y ? x : y; }, sh.ired);
+          last = block_all(last, [](int x, int y) { return x > y ? x : y; }, sh.ired, INT_MIN);
           chosen = last;
           break;
         }
@@ -1001,7 +1266,7 @@ template <int DT, bool VEC> struct FullRow {
           const int r = buckets - 1 - dd;
           if (r > rank && sh.u.hist.cnt[dd]) next = min(next, r);
         }
-        next = block_all(next, mn, sh.ired);
+        next = block_all(next, mn, sh.ired, INT_MAX);
         if (next == INT_MAX) { chosen = rank; break; }  // cannot happen: the region reaches the target
         rank = next;
       }
@@ -1011,8 +1276,8 @@ template <int DT, bool VEC> struct FullRow {
       double mb = 0, mbe = 0;
       for (int dd = threadIdx.x; dd < buckets; dd += BLOCK)
         if (dd > d) { mb += sh.u.hist.mass[dd]; mbe += double(sh.u.hist.cnt[dd]) * 0x1p-52 * sh.u.hist.mass[dd]; }
-      mb = block_all(mb, [](double x, double y) { return x + y; }, sh.dred);
-      mbe = block_all(mbe, [](double x, double y) { return x + y; }, sh.dred);
+      mb = block_all(mb, [](double x, double y) { return x + y; }, sh.dred, 0.0);
+      mbe = block_all(mbe, [](double x, double y) { return x + y; }, sh.dred, 0.0);
       const double slack = mbe + 1e-15 * mb + 1e-300;
       base_lo = base_lo + mb - slack;
       base_hi = base_hi + mb + slack;
@@ -1037,7 +1302,7 @@ template <int DT, bool VEC> struct FullRow {
   // Certified FP32 draw over tokens where in(t, v, ok) holds (excluded
   // removed), FP64 rescoring when the certificate fails. floor_id is a token
   // certainly in the set (or -1).
-  template <class In> __device__ int draw(int sub, int excluded, int floor_id, In&& in) {
+  template <class In> __device__ __forceinline__ int draw(int sub, int excluded, int floor_id, In&& in) {
     if (threadIdx.x == 0) {
       float floor = -INFINITY;
       if (floor_id >= 0) {
@@ -1081,11 +1346,7 @@ template <int DT, bool VEC> struct FullRow {
       w.others = fmaxf(fmaxf(x.others, y.others), l.hi);
       return w;
     };
-#pragma unroll
-    for (int m = WAVE / 2; m; m >>= 1) {
-      Pk o{xshfl(pk.mid, m), xshfl(pk.lo, m), xshfl(pk.hi, m), xshfl(pk.others, m), xshfl(pk.id, m)};
-      pk = op(pk, o);
-    }
+    pk = wave_all(pk, op, Pk{-INFINITY, -INFINITY, -INFINITY, -INFINITY, INT_MAX});
     __shared__ Pk s_pk[WAVES];
     __syncthreads();
     if (lane_id() == 0) s_pk[wave_id()] = pk;
@@ -1114,8 +1375,7 @@ template <int DT, bool VEC> struct FullRow {
     struct SI { double s; int id; };
     SI si{best, bid};
     auto op2 = [](SI x, SI y) { return (y.s > x.s || (y.s == x.s && y.id < x.id)) ? y : x; };
-#pragma unroll
-    for (int m = WAVE / 2; m; m >>= 1) si = op2(si, SI{xshfl(si.s, m), xshfl(si.id, m)});
+    si = wave_all(si, op2, SI{-INFINITY, INT_MAX});
     __syncthreads();
     if (lane_id() == 0) { sh.dred[wave_id()] = si.s; sh.ired[wave_id()] = si.id; }
     __syncthreads();
@@ -1127,7 +1387,7 @@ template <int DT, bool VEC> struct FullRow {
 
   // Finishes the row. Greedy rows without a full proposal and failed rows
   // never come here.
-  __device__ RowResult run(double maximum, int greedy, int runner_up_id, int valid) {
+  __device__ __forceinline__ RowResult run(double maximum, int greedy, int runner_up_id, int valid) {
     RowResult r{0, 1, -1, -1, ES_OK, ES_OK};
     const bool full_q = p.full_q != 0;
     // ---- The actual proposal q of a full-q draft row (reference.py:206-216). ----
@@ -1140,9 +1400,9 @@ template <int DT, bool VEC> struct FullRow {
         qvalid += y > neg_inf<W>();
         qm = y > qm ? y : qm;
       });
-      qbad = block_all(qbad, [](int x, int y) { return x | y; }, sh.ired);
-      qvalid = block_all(qvalid, [](int x, int y) { return x + y; }, sh.ired);
-      qm = block_all(qm, [](W x, W y) { return x > y ? x : y; }, sh.u.r.red_w);
+      qbad = block_all(qbad, [](int x, int y) { return x | y; }, sh.ired, 0);
+      qvalid = block_all(qvalid, [](int x, int y) { return x + y; }, sh.ired, 0);
+      qm = block_all(qm, [](W x, W y) { return x > y ? x : y; }, sh.u.r.red_w, neg_inf<W>());
       int qstatus = qbad ? ES_INVALID_INPUT : qvalid == 0 ? ES_NO_VALID_TOKEN : ES_OK;
       qmax = double(qm);
       if (qstatus == ES_OK) {
@@ -1178,7 +1438,7 @@ template <int DT, bool VEC> struct FullRow {
     auto kept = [&](int, W v, bool ok) { return valid_tok(v, ok) && tp.kept(v, tp.x32(v)); };
     int nk = 0;
     each<false>([&](int t, W v, bool ok) { nk += kept(t, v, ok); });
-    nk = block_all(nk, [](int x, int y) { return x + y; }, sh.ired);
+    nk = block_all(nk, [](int x, int y) { return x + y; }, sh.ired, 0);
     // ---- Top-k: an exact cut at the k-th token (reference.py:67-71). ----
     u128 cut = 0;  // keep ck >= cut
     if (p.top_k > 0 && p.top_k < nk) cut = select_nth(int(p.top_k), kept);
@@ -1220,9 +1480,9 @@ template <int DT, bool VEC> struct FullRow {
             c = (tt - s) - d; s = tt;
             e += w * (X_ERR * (1.f + fabsf(x)));
           });
-          const double sum = block_all(double(s) - double(c), [](double x, double y) { return x + y; }, sh.dred);
-          const double et = block_all(double(e), [](double x, double y) { return x + y; }, sh.dred);
-          pruned = block_all(pruned, [](int x, int y) { return x + y; }, sh.ired);
+          const double sum = block_all(double(s) - double(c), [](double x, double y) { return x + y; }, sh.dred, 0.0);
+          const double et = block_all(double(e), [](double x, double y) { return x + y; }, sh.dred, 0.0);
+          pruned = block_all(pruned, [](int x, int y) { return x + y; }, sh.ired, 0);
           const double esp = 1.01 * et + 4.8e-7 * sum + pruned * SUM_PRUNE_W;
           const double wx = exp(tp.x64(vx));
           const double qx_lo = full_q ? wq_draft / sq * (1 - 1e-15) : 1.0, qx_hi = full_q ? wq_draft / sq * (1 + 1e-15) : 1.0;
@@ -1272,8 +1532,7 @@ template <int DT, bool VEC> struct FullRow {
       struct SI { double s; int id; };
       SI si{best, bid};
       auto op2 = [](SI x, SI y) { return (y.s > x.s || (y.s == x.s && y.id < x.id)) ? y : x; };
-#pragma unroll
-      for (int m = WAVE / 2; m; m >>= 1) si = op2(si, SI{xshfl(si.s, m), xshfl(si.id, m)});
+      si = wave_all(si, op2, SI{-INFINITY, INT_MAX});
       __syncthreads();
       if (lane_id() == 0) { sh.dred[wave_id()] = si.s; sh.ired[wave_id()] = si.id; }
       __syncthreads();
@@ -1289,30 +1548,85 @@ template <int DT, bool VEC> struct FullRow {
 };
 
 // ---------------------------------------------------------------------------
-// Register-tile helpers of the slice pass. Token (i, j) of a thread is
-// 4 * (gb + BLOCK * i) + j; IDs rise with (i, thread, j).
-
-// One bit per token of the tile where pred(value, id) holds.
-template <class W, int G, class Pred>
-__device__ __forceinline__ uint64_t collect_bits(const W (&v)[G][4], Pred&& pred, int gb = 0) {
-  uint32_t lo = 0, hi = 0;
+// The slice's tokens in the register tile's order. Token (i, j) of a thread
+// is 4 * (gb + BLOCK * i) + j, so IDs rise with (i, thread, j); tokens that
+// are masked or outside the slice have the value -inf. TileVisit walks the
+// tile in registers; MemVisit reads the same tokens again from memory, for the
+// rare paths that run after the tile is gone (so the tile's registers are not
+// held through them).
+template <class W, int G> struct TileVisit {
+  const W (&v)[G][4];
+  int gb;
+  template <class F> __device__ __forceinline__ void operator()(F&& f) const {
 #pragma unroll
-  for (int i = 0; i < G; ++i) {
+    for (int i = 0; i < G; ++i) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int k = 4 * i + j;
-      const uint32_t bit = pred(v[i][j], 4 * (gb + BLOCK * i) + j) && v[i][j] > neg_inf<W>();
-      if (k < 32) lo |= bit << k; else hi |= bit << (k - 32);
+      for (int j = 0; j < 4; ++j) f(i, j, v[i][j], 4 * (gb + BLOCK * i) + j);
     }
   }
-  return (uint64_t(hi) << 32) | lo;
+};
+
+template <int DT, bool VEC, int G> struct MemVisit {
+  using W = typename Ty<DT>::W;
+  RowView<DT, VEC> view;
+  const int32_t* mask;  // the row's mask words, or null
+  int64_t mask_s1;
+  int gb, g1, groups;
+  __device__ __forceinline__ MemVisit(const es_arguments& a, int64_t row, const RowView<DT, VEC>& v, int gb_, int g1_,
+                                      int groups_)
+      : view(v), mask(a.mask ? a.mask + row * a.mask_s0 : nullptr), mask_s1(a.mask_s1), gb(gb_), g1(g1_),
+        groups(groups_) {}
+  template <class F> __device__ __forceinline__ void operator()(F&& f) const {
+#pragma unroll 1
+    for (int i = 0; i < G; ++i) {
+      const int g = gb + BLOCK * i, gc = min(g, groups - 1);
+      W x[4];
+      view.load(gc, x);
+      uint32_t mb = g < g1 ? 0xfu : 0u;
+      if (mask && 4 * gc < view.vocab) mb &= uint32_t(mask[int64_t((4 * gc) >> 5) * mask_s1]) >> ((4 * gc) & 31);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) f(i, j, ((mb >> j) & 1u) ? x[j] : neg_inf<W>(), 4 * g + j);
+    }
+  }
+};
+
+// One bit per token where pred(value, id) holds (valid tokens only).
+template <class W, class Visit, class Pred>
+__device__ __forceinline__ uint64_t collect_bits(const Visit& visit, Pred&& pred) {
+  uint64_t bits = 0;
+  visit([&](int i, int j, W x, int t) {
+    if (pred(x, t) && x > neg_inf<W>()) bits |= 1ull << (4 * i + j);
+  });
+  return bits;
+}
+
+// Appends the tokens whose bits are set to the block's list in LDS (in any
+// order: the list is sorted afterwards) and returns the block's total.
+template <class W, class Visit>
+__device__ __forceinline__ int append_taken(const Visit& visit, uint64_t bits, Shared<W>& sh) {
+  const int mine = __popcll(bits);
+  int slot = mine ? atomicAdd(&sh.appended, mine) : 0;
+  if (mine) {
+    visit([&](int i, int j, W x, int t) {
+      if ((bits >> (4 * i + j)) & 1ull) {
+        if (slot < LIST_LIMIT) {
+          sh.u.list.v[slot] = x;
+          sh.u.list.id[slot] = t;
+        }
+        ++slot;
+      }
+    });
+  }
+  __syncthreads();
+  return sh.appended;
 }
 
 // The slice's L-th valid token in (value desc, ID asc) order, given that at
 // least L valid tokens are >= floor: radix selection over the value's order
-// key among those tokens, then the tie broken by ID in (i, thread, j) order.
-template <class W, int G>
-__device__ void slice_cut(const W (&v)[G][4], int gb, int L, W floor, Shared<W>& sh, W* out_v, int* out_id) {
+// key among those tokens (8-bit digits), then the tie broken by ID, which is
+// the (i, thread, j) order of the visit.
+template <class W, int G, class Visit>
+__device__ __forceinline__ void slice_cut(const Visit& visit, int L, W floor, Shared<W>& sh, W* out_v, int* out_id) {
   using K = typename std::conditional<sizeof(W) == 8, uint64_t, uint32_t>::type;
   constexpr int KB = int(sizeof(K) * 8);
   // Scratch in the block's union: 256 counters, then G x BLOCK tie counts.
@@ -1324,17 +1638,12 @@ __device__ void slice_cut(const W (&v)[G][4], int gb, int L, W floor, Shared<W>&
     __syncthreads();
     hist[threadIdx.x] = 0;
     __syncthreads();
-#pragma unroll
-    for (int i = 0; i < G; ++i) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const W x = v[i][j];
-        if (x >= floor && x > neg_inf<W>()) {
-          const K k = order_key(x);
-          if ((k & known) == prefix) atomicAdd(&hist[int(k >> shift) & 255], 1u);
-        }
+    visit([&](int, int, W x, int) {
+      if (x >= floor && x > neg_inf<W>()) {
+        const K k = order_key(x);
+        if ((k & known) == prefix) atomicAdd(&hist[int(k >> shift) & 255], 1u);
       }
-    }
+    });
     __syncthreads();
     const int c = int(hist[255 - threadIdx.x]);  // descending digits, one per thread
     int tot;
@@ -1348,13 +1657,8 @@ __device__ void slice_cut(const W (&v)[G][4], int gb, int L, W floor, Shared<W>&
   const W cut_v = key_value(prefix);
   // `need` tokens with value cut_v are taken, the lowest IDs first.
   int* ties = reinterpret_cast<int*>(&sh.u) + 256;  // [G][BLOCK]
-#pragma unroll
-  for (int i = 0; i < G; ++i) {
-    int c = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) c += v[i][j] == cut_v;
-    ties[i * BLOCK + threadIdx.x] = c;
-  }
+  for (int i = 0; i < G; ++i) ties[i * BLOCK + threadIdx.x] = 0;
+  visit([&](int i, int, W x, int) { ties[i * BLOCK + threadIdx.x] += x == cut_v; });
   __syncthreads();
   if (threadIdx.x == 0) {
     int before = 0, gi = 0;
@@ -1379,13 +1683,9 @@ __device__ void slice_cut(const W (&v)[G][4], int gb, int L, W floor, Shared<W>&
   __syncthreads();
   if (int(threadIdx.x) == owner) {
     int seen = 0, id = INT_MAX;
-#pragma unroll
-    for (int i = 0; i < G; ++i) {
-      if (i != gi) continue;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (v[i][j] == cut_v && ++seen == rank) id = 4 * (gb + BLOCK * i) + j;
-    }
+    visit([&](int i, int, W x, int t) {
+      if (i == gi && x == cut_v && ++seen == rank) id = t;
+    });
     sh.ck = id;
   }
   __syncthreads();
@@ -1400,7 +1700,6 @@ template <int DT, bool VEC, int G>
 __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
   using W = typename Ty<DT>::W;
   __shared__ Shared<W> sh;
-  __shared__ Params sp;
   const int tid = threadIdx.x;
   const int lane = lane_id();
 
@@ -1427,9 +1726,16 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
   const RowView<DT, VEC> view(a.target, row, vocab);
   const int g0 = slice * pl.gps, g1 = min(g0 + pl.gps, pl.groups);
 
-  // Loads first: the metadata checks below overlap them. Every lane loads (an
-  // index clamped into the row), so there is no branch per load; tokens
-  // outside the slice are then set to -inf.
+  // The first chunk of the offsets, then the tile: waiting for the offsets
+  // (vmcnt counts loads in issue order) leaves the tile loads in flight. Every
+  // lane loads the tile (an index clamped into the row), so there is no branch
+  // per load; tokens outside the slice are then set to -inf.
+  int64_t x0 = 0, x1 = 0;
+  if (tid < a.requests) {
+    x0 = at(a.cu_rows, tid);
+    x1 = at(a.cu_rows, tid + 1);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   W v[G][4];
   uint64_t mbits = ~0ull;
   const int gb = g0 + tid;
@@ -1446,8 +1752,8 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[i][j] = in ? v[i][j] : neg_inf<W>();
   }
-  block_params(a, row, &sp, sh);
-  const Params p = sp;
+  Params p;
+  slice_lookup(a, row, x0, x1, &p, sh);
   if (p.status != ES_OK) {
     if (slice == 0) skip_row(a, row, sh);
     return;
@@ -1461,90 +1767,124 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) bad_l |= isnan(v[i][j]) || v[i][j] == W(INFINITY);
   }
-  if (a.mask) {
+  // Unconditional (mbits is all ones without a mask): a branch here would keep
+  // a masked and an unmasked copy of the tile alive at its join.
 #pragma unroll
-    for (int i = 0; i < G; ++i) {
+  for (int i = 0; i < G; ++i) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) v[i][j] = ((mbits >> (4 * i + j)) & 1ull) ? v[i][j] : neg_inf<W>();
-    }
+    for (int j = 0; j < 4; ++j) v[i][j] = ((mbits >> (4 * i + j)) & 1ull) ? v[i][j] : neg_inf<W>();
   }
   // From here on a token is valid exactly when its value is above -inf (a NaN
-  // token only occurs in an invalid row, whose other results are unused).
+  // token only occurs in an invalid row, whose other results are unused). The
+  // thread's maximum keeps its lowest ID: IDs rise with (i, j).
+  int fid_l = INT_MAX;
 #pragma unroll
   for (int i = 0; i < G; ++i) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       valid_l += v[i][j] > neg_inf<W>();
-      mx = v[i][j] > mx ? v[i][j] : mx;
+      const bool up = v[i][j] > mx;
+      fid_l = up ? 4 * (gb + BLOCK * i) + j : fid_l;
+      mx = up ? v[i][j] : mx;
     }
   }
-  const int valid_w = wave_all(valid_l, [](int x, int y) { return x + y; });
-  const int bad_w = wave_all(bad_l, [](int x, int y) { return x | y; });
-  if (lane == 0) { sh.u.r.red_i[wave_id()] = valid_w; sh.u.r.red_i2[wave_id()] = bad_w; }
-  const W wmax = wave_all(mx, [](W x, W y) { return x > y ? x : y; });
-  if (lane == 0) sh.u.r.red_w[wave_id()] = wmax;
-  __syncthreads();
-  int valid = 0, bad = 0;
-  W smax = neg_inf<W>();
-  for (int w = 0; w < WAVES; ++w) {
-    valid += sh.u.r.red_i[w];
-    bad |= sh.u.r.red_i2[w];
-    smax = sh.u.r.red_w[w] > smax ? sh.u.r.red_w[w] : smax;
-  }
-  // The lowest ID holding the slice maximum: tokens equal to it are rare, so
-  // the search costs one compare per token behind a wave-uniform branch.
-  int first_id = INT_MAX;
-#pragma unroll
-  for (int i = 0; i < G; ++i) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bool hit = v[i][j] == smax && smax > neg_inf<W>();
-      first_id = hit && first_id == INT_MAX ? 4 * (gb + BLOCK * i) + j : first_id;
-    }
-  }
-  first_id = block_all(first_id, [](int x, int y) { return x < y ? x : y; }, sh.ired);
-
-  // ---- Candidates for a list row. ----
+  // What the candidate pass takes is decided by the request's scalars.
   const int list_max = a.list_max;
-  const bool positive_t = p.temperature > 0;
   int need = 0;  // 0: no candidates; > 0: the slice's top `need`; -1: all valid if they fit
-  if (positive_t && list_max > 0 && !p.full_q && !bad) {
+  if (p.temperature > 0 && list_max > 0 && !p.full_q) {
     if (p.top_k >= 1 && p.top_k <= list_max) need = int(p.top_k);
     else if (p.top_p < 1 && p.min_p == 0) need = TOPP_SLICE_NEED;
     else need = -1;
   }
+  const int L = need > 0 ? min(need, pl.cap_slice) : 0;
+  // Top-k rows with k <= 64 (and within the slice capacity) are finished by
+  // one wave of the merging block from sorted per-slice lists.
+  const bool sorted_list = need > 0 && L == need && need <= WAVE;
+  // The j-th largest thread maximum of the wave, j = ceil(L / 4): at least L
+  // valid tokens of the slice are >= the smallest of the four waves' values.
+  W tw = neg_inf<W>();
+  if (L > 0) tw = key_value(wave_kth_largest(order_key(mx), (L + WAVES - 1) / WAVES));
+  // One exchange between the waves: counts, flags, the maximum with its
+  // lowest ID and the thresholds.
+  const int valid_w = wave_all(valid_l, [](int x, int y) { return x + y; }, 0);
+  const int bad_w = __ballot(bad_l) != 0;
+  struct MI { W v; int id; };
+  const MI wm = wave_all(MI{mx, fid_l}, [](MI x, MI y) { return (y.v > x.v || (y.v == x.v && y.id < x.id)) ? y : x; },
+                         MI{neg_inf<W>(), INT_MAX});
+  const W wmax = wm.v;
+  const int wid = wm.id;
+  if (lane == 0) {
+    sh.st_max[wave_id()] = wmax;
+    sh.st_id[wave_id()] = wid;
+    sh.st_valid[wave_id()] = valid_w;
+    sh.st_bad[wave_id()] = bad_w;
+    sh.st_thr[wave_id()] = tw;
+  }
+  if (tid == 0) sh.appended = 0;
+  __syncthreads();
+  int valid = 0, bad = 0, first_id = INT_MAX;
+  W smax = neg_inf<W>(), thr_all = W(INFINITY);
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) {
+    valid += sh.st_valid[w];
+    bad |= sh.st_bad[w];
+    if (sh.st_max[w] > smax || (sh.st_max[w] == smax && sh.st_id[w] < first_id)) {
+      smax = sh.st_max[w];
+      first_id = sh.st_id[w];
+    }
+    thr_all = sh.st_thr[w] < thr_all ? sh.st_thr[w] : thr_all;
+  }
+  if (bad) need = 0;
+
+  // ---- Candidates for a list row. ----
+  // The tile serves the first selection; anything after it re-reads memory.
+  const TileVisit<W, G> tile{v, gb};
+  const MemVisit<DT, VEC, G> mem(a, row, view, gb, g1, pl.groups);
   double frontier = -INFINITY, psum = 0, perr = 0;
   int n_cand = 0, pruned = 0, fid = INT_MAX;
-  if (need != 0) {
-    const int cap = pl.cap_slice;
-    W thr = neg_inf<W>();
-    if (need > 0 && need < valid) {
-      // The j-th largest thread maximum of each wave, j = ceil(L / 4): at least
-      // L valid tokens are >= the smallest of the four (L = min(need, cap)).
-      const int L = min(need, cap);
-      const int j = (L + WAVES - 1) / WAVES;
-      W x = mx;
-#pragma unroll
-      for (int k = 2; k <= WAVE; k <<= 1) {
-#pragma unroll
-        for (int jj = k >> 1; jj > 0; jj >>= 1) {
-          const W y = xshfl(x, jj);
-          const bool lower = (lane & jj) == 0, desc = (lane & k) == 0;
-          const W hi = x > y ? x : y, lo = x > y ? y : x;
-          x = (lower == desc) ? hi : lo;
-        }
-      }
-      const W tw = __shfl(x, j - 1, WAVE);
+  if (sorted_list && need > 0) {
+    // Top-k rows: the slice's first min(k, valid) tokens, sorted, for the merge wave.
+    const W thr = need < valid ? thr_all : neg_inf<W>();
+    const W take_from = thr > W(-3.4028234663852886e38) ? thr : W(-3.4028234663852886e38);
+    int total = append_taken<W>(tile, collect_bits<W>(tile, [&](W x, int) { return x >= take_from; }), sh);
+    if (total > WAVE) {
+      // Too many (ties, or a low threshold): exactly the first L instead.
+      W cut_v;
+      int cut_id;
+      slice_cut<W, G>(mem, L, take_from, sh, &cut_v, &cut_id);
+      if (tid == 0) sh.appended = 0;
       __syncthreads();
-      if (lane == 0) sh.u.r.red_w[wave_id()] = tw;
-      __syncthreads();
-      thr = sh.u.r.red_w[0];
-      for (int w = 1; w < WAVES; ++w) thr = sh.u.r.red_w[w] < thr ? sh.u.r.red_w[w] : thr;
+      total = append_taken<W>(
+          mem, collect_bits<W>(mem, [&](W x, int t) { return x > cut_v || (x == cut_v && t <= cut_id); }), sh);
     }
+    n_cand = min(total, L);
+    if (wave_id() == 0) {
+      const int n = min(total, WAVE);
+      W cv = neg_inf<W>();
+      int cid = INT_MAX;
+      if (lane < n) { cv = sh.u.list.v[lane]; cid = sh.u.list.id[lane]; }
+      const int rank = wave_rank(cv, cid, n);
+      if (lane < n && rank < n_cand) {
+        Cand<W> c{};
+        c.v = cv;
+        c.id = cid;
+        publish(candidates<W>(a, row) + slice * pl.cap_slice + rank, c);
+      }
+      // Complete down to the last stored token, or entirely.
+      const uint64_t last = __ballot(lane < n && rank == n_cand - 1);
+      if (valid > n_cand && last) {
+        const int src = __ffsll((unsigned long long)last) - 1;
+        frontier = double(lane_read(cv, src));
+        fid = lane_read(cid, src);
+      }
+    }
+  } else if (need != 0) {
+    const int cap = pl.cap_slice;
+    W thr = need > 0 && need < valid ? thr_all : neg_inf<W>();
     // Tokens at or above the threshold: one bit per token of this thread.
     // -inf is never taken: the threshold is raised to the lowest finite value.
     const W take_from = thr > W(-3.4028234663852886e38) ? thr : W(-3.4028234663852886e38);
-    uint64_t take_bits = collect_bits<W, G>(v, [&](W x, int) { return x >= take_from; });
+    uint64_t take_bits = collect_bits<W>(tile, [&](W x, int) { return x >= take_from; });
     int mine = __popcll(take_bits);
     int total;
     int offset = block_scan_add(mine, sh.ired, &total) - mine;
@@ -1555,8 +1895,8 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
       const int L = min(need, cap);
       W cut_v;
       int cut_id;
-      slice_cut<W, G>(v, gb, L, take_from, sh, &cut_v, &cut_id);
-      take_bits = collect_bits<W, G>(v, [&](W x, int t) { return x > cut_v || (x == cut_v && t <= cut_id); }, gb);
+      slice_cut<W, G>(mem, L, take_from, sh, &cut_v, &cut_id);
+      take_bits = collect_bits<W>(mem, [&](W x, int t) { return x > cut_v || (x == cut_v && t <= cut_id); });
       mine = __popcll(take_bits);
       offset = block_scan_add(mine, sh.ired, &total) - mine;
       thr = cut_v;
@@ -1593,26 +1933,21 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
       const bool slow = !(inv_t < 1e30f);
       float s = 0, c = 0, e = 0;
       int pr = 0;
-#pragma unroll
-      for (int i = 0; i < G; ++i) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const W x = v[i][j];
-          float xl;
-          if constexpr (sizeof(W) == 8) xl = float((double(x) - ms) / p.temperature);
-          else xl = slow ? float(double(x - float(ms)) / p.temperature) : (x - float(ms)) * inv_t;
-          const bool ok = x > neg_inf<W>();
-          const bool counted = ok && xl >= SUM_PRUNE;
-          pr += ok && !counted;
-          const float w = expf(counted ? xl : -100.f) * (counted ? 1.f : 0.f);
-          const float d = w - c, t2 = s + d;
-          c = (t2 - s) - d; s = t2;
-          e += w * (X_ERR * (1.f + fabsf(counted ? xl : 0.f)));
-        }
-      }
-      psum = block_all(double(s) - double(c), [](double x, double y) { return x + y; }, sh.dred);
-      perr = block_all(double(e), [](double x, double y) { return x + y; }, sh.dred);
-      pruned = block_all(pr, [](int x, int y) { return x + y; }, sh.ired);
+      mem([&](int, int, W x, int) {
+        float xl;
+        if constexpr (sizeof(W) == 8) xl = float((double(x) - ms) / p.temperature);
+        else xl = slow ? float(double(x - float(ms)) / p.temperature) : (x - float(ms)) * inv_t;
+        const bool ok = x > neg_inf<W>();
+        const bool counted = ok && xl >= SUM_PRUNE;
+        pr += ok && !counted;
+        const float w = expf(counted ? xl : -100.f) * (counted ? 1.f : 0.f);
+        const float d = w - c, t2 = s + d;
+        c = (t2 - s) - d; s = t2;
+        e += w * (X_ERR * (1.f + fabsf(counted ? xl : 0.f)));
+      });
+      psum = block_all(double(s) - double(c), [](double x, double y) { return x + y; }, sh.dred, 0.0);
+      perr = block_all(double(e), [](double x, double y) { return x + y; }, sh.dred, 0.0);
+      pruned = block_all(pr, [](int x, int y) { return x + y; }, sh.ired, 0);
     }
   }
   if (tid == 0) {
@@ -1633,8 +1968,26 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
   }
   if (!arrive(&counters(a, row)->slices, uint32_t(pl.slices), &sh.flag)) return;
 
-  // ---- The last slice block merges the row (slice order, wave 0). ----
+  // ---- The last slice block merges the row. ----
+  // Wave 1 checks the request's per-row metadata while wave 0 fetches the
+  // slices' summaries (and a top-k row's sorted lists, every slot at once)
+  // and merges them in slice order.
+  load_row_rng(a, row, &p);
+  if (wave_id() == 1) {
+    const bool ok = request_rows_ok(a, p);
+    if (lane == 0) sh.meta_bad = !ok;
+  }
   if (wave_id() == 0) {
+    Cand<W> pre[WAVE_BATCH];
+    if (sorted_list) {
+      const Cand<W>* cands = candidates<W>(a, row);
+#pragma unroll
+      for (int r = 0; r < WAVE_BATCH; ++r) {
+        const int idx = lane + WAVE * r;
+        pre[r] = Cand<W>{};
+        if (idx < pl.slices * L) pre[r] = fetch(cands + (idx / L) * pl.cap_slice + idx % L);
+      }
+    }
     SlicePart q;
     q.max_v = -INFINITY; q.second_v = -INFINITY; q.frontier = -INFINITY; q.tau = -INFINITY;
     q.sum = 0; q.err = 0; q.max_id = INT_MAX; q.second_id = INT_MAX; q.valid = 0; q.n_cand = 0; q.pruned = 0; q.flags = 0;
@@ -1647,21 +2000,18 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
       const bool second_l = before(l.v1, l.i1, w.v2, w.i2);
       return T2d{w.v1, w.i1, second_l ? l.v1 : w.v2, second_l ? l.i1 : w.i2};
     };
-    T2d t2{q.max_v, q.max_id, q.second_v, q.second_id};
-#pragma unroll
-    for (int m = WAVE / 2; m; m >>= 1) t2 = top2d(t2, T2d{xshfl(t2.v1, m), xshfl(t2.i1, m), xshfl(t2.v2, m), xshfl(t2.i2, m)});
-    const int vsum = wave_all(q.valid, [](int x, int y) { return x + y; });
-    const int bsum = wave_all(q.flags, [](int x, int y) { return x | y; });
+    // Slices report their maximum only: the runner-up is the best other slice maximum.
+    T2d t2{q.max_v, q.max_id, -INFINITY, INT_MAX};
+    t2 = wave_all(t2, top2d, T2d{-INFINITY, INT_MAX, -INFINITY, INT_MAX});
+    const int vsum = wave_all(q.valid, [](int x, int y) { return x + y; }, 0);
+    const int bsum = wave_all(q.flags, [](int x, int y) { return x | y; }, 0);
     // The earliest frontier in (value desc, ID asc) order: every slice is
     // complete down to it.
     struct Fr { double v; int id; };
     Fr fr{lane < pl.slices ? q.frontier : -INFINITY, lane < pl.slices ? q.second_id : INT_MAX};
-#pragma unroll
-    for (int m = WAVE / 2; m; m >>= 1) {
-      const Fr o{xshfl(fr.v, m), xshfl(fr.id, m)};
-      fr = (o.v > fr.v || (o.v == fr.v && o.id < fr.id)) ? o : fr;
-    }
-    const int nct = wave_all(q.n_cand, [](int x, int y) { return x + y; });
+    fr = wave_all(fr, [](Fr x, Fr o) { return (o.v > x.v || (o.v == x.v && o.id < x.id)) ? o : x; },
+                  Fr{-INFINITY, INT_MAX});
+    const int nct = wave_all(q.n_cand, [](int x, int y) { return x + y; }, 0);
     // Top-p sums rescaled from slice maxima to the row maximum (FP64).
     double s_sum = 0, s_err = 0;
     int s_pr = q.pruned;
@@ -1671,17 +2021,33 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
       if (shift > 700) { s_err = (q.sum + q.err) * scale + q.pruned * SUM_PRUNE_W; s_pr = 0; }
       else { s_sum = q.sum * scale; s_err = (1.01 * q.err + 4.8e-7 * q.sum) * scale * (1 + 1e-14); }
     }
-    s_sum = wave_all(s_sum, [](double x, double y) { return x + y; });
-    s_err = wave_all(s_err, [](double x, double y) { return x + y; });
-    s_pr = wave_all(s_pr, [](int x, int y) { return x + y; });
+    s_sum = wave_all(s_sum, [](double x, double y) { return x + y; }, 0.0);
+    s_err = wave_all(s_err, [](double x, double y) { return x + y; }, 0.0);
+    s_pr = wave_all(s_pr, [](int x, int y) { return x + y; }, 0);
     if (lane == 0) {
       sh.maximum = t2.v1; sh.greedy = t2.i1; sh.runner_up = t2.v2; sh.runner_up_id = t2.i2;
       sh.valid = vsum; sh.bad = bsum; sh.frontier = fr.v; sh.frontier_id = fr.id; sh.n_cand_total = nct;
       sh.sum = s_sum;
       sh.err = s_err + s_pr * SUM_PRUNE_W + 1e-15 * s_sum;
     }
+    // A top-k row is finished here by this wave.
+    int wdone = 0;
+    RowResult wr{0, 1, -1, -1, ES_OK, ES_OK};
+    if (sorted_list && bsum == 0 && vsum > 0) {
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      wdone = wave_topk(a, row, p, sh, pre, pl.slices, pl.cap_slice, L, t2.v1, fr.v, fr.id, vsum, &wr);
+    }
+    if (lane == 0) {
+      sh.wdone = wdone;
+      sh.wres = wr;
+    }
   }
   __syncthreads();
+  if (sh.meta_bad) {
+    // The request block reports the request as invalid.
+    skip_row(a, row, sh);
+    return;
+  }
   const int status = sh.bad ? ES_INVALID_INPUT : sh.valid == 0 ? ES_NO_VALID_TOKEN : ES_OK;
   if (tid == 0) {
     RowState* st = row_state(a, row);
@@ -1701,9 +2067,14 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
       result.p = accept ? 1.0 : 0.0;
       if (!accept) result.residual = sh.greedy;
     }
+  } else if (sorted_list && sh.wdone == 1) {
+    route = 3;
+    result = sh.wres;
   } else {
     bool done = false;
-    if (p.temperature > 0 && !p.full_q && list_max > 0) {
+    if (sorted_list && sh.wdone < 0) {
+      why = 7;  // a rounding the wave could not certify: the full-row path decides
+    } else if (p.temperature > 0 && !p.full_q && list_max > 0) {
       const int valid_all = sh.valid;
       const int n_keep = p.top_k > 0 && p.top_k < valid_all ? int(p.top_k) : valid_all;
       const bool topk_list = n_keep <= list_max;

@@ -39,7 +39,7 @@ __device__ __forceinline__ void sacc_add(unsigned long long* limbs, double w) {
 // Run by one thread after the adds are visible: the correctly rounded sum.
 // Propagates carries in place (the limbs then hold 32-bit digits), then reads
 // the top 64 bits and a sticky flag word by word.
-__device__ inline double sacc_round(unsigned long long* limbs) {
+__device__ __forceinline__ double sacc_round(unsigned long long* limbs) {
   unsigned long long carry = 0;
   int top = -1;
   for (int i = 0; i < SACC_LIMBS; ++i) {
