@@ -437,6 +437,27 @@ __device__ __forceinline__ void slice_lookup(const es_arguments& a, int64_t row,
   p->rng.stream = uint32_t(stream);
 }
 
+// What the candidate pass takes for a row, decided by the request's scalars
+// (the slice blocks and the finishing block compute it alike): need = 0 no
+// candidates, > 0 the slice's top `need`, -1 every valid token if they fit.
+struct ListPlan {
+  int need, L;
+  bool sorted_list;  // a top-k row (k <= 64, within the slice capacity) finished by one wave
+  bool need_topp;    // a top-p list: the slices also sum their kept weights
+};
+__device__ __forceinline__ ListPlan list_plan(const Params& p, int list_max, int cap) {
+  ListPlan lp{0, 0, false, false};
+  if (p.temperature > 0 && list_max > 0 && !p.full_q) {
+    if (p.top_k >= 1 && p.top_k <= list_max) lp.need = int(p.top_k);
+    else if (p.top_p < 1 && p.min_p == 0) lp.need = TOPP_SLICE_NEED;
+    else lp.need = -1;
+  }
+  lp.L = lp.need > 0 ? min(lp.need, cap) : 0;
+  lp.sorted_list = lp.need > 0 && lp.L == lp.need && lp.need <= WAVE;
+  lp.need_topp = lp.need == TOPP_SLICE_NEED && p.top_p < 1 && !(p.top_k >= 1 && p.top_k <= list_max);
+  return lp;
+}
+
 // The per-row metadata of a request (positions and draft IDs in range),
 // checked by one wave.
 __device__ __forceinline__ bool request_rows_ok(const es_arguments& a, const Params& p) {
@@ -523,19 +544,16 @@ __device__ __forceinline__ void finalize_request(const es_arguments& a, int64_t 
   }
 }
 
-// Every row arrives once per call; the last one totals the rows' FP64
-// recomputations into workspace word 1.
-template <class W> __device__ __forceinline__ void grid_arrive(const es_arguments& a, Shared<W>& sh) {
-  if (arrive(&counters(a, 0)->grid, uint32_t(a.rows), &sh.flag)) {
-    unsigned total = 0;
-    for (int64_t r = threadIdx.x; r < a.rows; r += BLOCK) total += unsigned(ld_dev32(&row_state(a, r)->fallbacks));
-    total = block_all(total, [](unsigned x, unsigned y) { return x + y; }, reinterpret_cast<unsigned*>(sh.ired), 0u);
-    if (threadIdx.x == 0) reinterpret_cast<uint32_t*>(a.workspace)[1] = total;
-  }
+// The call's FP64 recomputation count, workspace word 1: zeroed by the first
+// kernel, then added to by the full-row kernel (which runs after it): its
+// block 0 adds what the rows finished in the first kernel recorded, and each
+// full-row block adds its own row's.
+__device__ __forceinline__ void add_fallbacks(const es_arguments& a, unsigned n) {
+  if (n) atomicAdd(reinterpret_cast<unsigned*>(a.workspace) + 1, n);
 }
 
-// Publishes a finished row and runs the request commit and the call's
-// fallback total when this row completes them. Every thread calls it.
+// Publishes a finished row and runs the request commit when this row
+// completes its request. Every thread calls it.
 template <class W>
 __device__ __forceinline__ void complete_row(const es_arguments& a, int64_t row, const Params& p,
                                              const RowResult& result, int fallbacks, int route, Shared<W>& sh) {
@@ -562,17 +580,14 @@ __device__ __forceinline__ void complete_row(const es_arguments& a, int64_t row,
   } else if (arrive(&counters(a, p.begin)->request, uint32_t(nrows), &sh.flag)) {
     if (wave_id() == 0) finalize_request(a, p.req);
   }
-  grid_arrive(a, sh);
 }
 
-template <class W>
-__device__ __forceinline__ void skip_row(const es_arguments& a, int64_t row, Shared<W>& sh) {
+__device__ __forceinline__ void skip_row(const es_arguments& a, int64_t row) {
   if (threadIdx.x == 0) {
     RowState* st = row_state(a, row);
     st->part = PART_SKIP;
-    st_dev32(&st->fallbacks, 0);
+    st->fallbacks = 0;
   }
-  grid_arrive(a, sh);
 }
 
 // ---------------------------------------------------------------------------
@@ -894,30 +909,51 @@ template <class W> __device__ __forceinline__ int wave_rank(W v, int id, int n) 
   return rank;
 }
 
+// The slot layout of the merge wave's prefetch: slice s's first `pref`
+// candidates at slots s * pref + i; idx / pref by a 20-bit reciprocal, exact
+// for idx < 2^12 and pref < 256.
+struct SlotMap {
+  int pref;
+  uint32_t inv;
+  __device__ __forceinline__ explicit SlotMap(int pref_) : pref(pref_), inv(((1u << 20) + uint32_t(pref_) - 1) / uint32_t(pref_)) {}
+  __device__ __forceinline__ int slice(int idx) const { return int((uint64_t(uint32_t(idx)) * inv) >> 20); }
+};
+
 template <class W>
 __device__ __forceinline__ int wave_topk(const es_arguments& a, int64_t row, const Params& p, Shared<W>& sh,
-                                         const Cand<W> (&pre)[WAVE_BATCH], int slices, int cap, int k, double M,
-                                         double F, int F_id, int valid_all, RowResult* out) {
+                                         const Cand<W> (&pre)[WAVE_BATCH], const SlotMap& map, int slices, int cap,
+                                         double M, double F, int F_id, int valid_all, RowResult* out) {
   using K = typename std::conditional<sizeof(W) == 8, uint64_t, uint32_t>::type;
   const int lane = lane_id();
-  const int slots = slices * k;
-  if (slots > WAVE * WAVE_BATCH) return 0;
-  // The slice of a slot (idx / k without a division: idx < 2^12, k <= 64, so
-  // the 20-bit reciprocal is exact).
-  const uint32_t inv_k = ((1u << 20) + uint32_t(k) - 1) / uint32_t(k);
-  // The union at or before F, compacted into LDS in slot order.
+  const int pref = map.pref;
+  // The union at or before F, compacted into LDS.
   int n_u = 0;
+  auto add = [&](bool take, const Cand<W>& c) {
+    const uint64_t mk = __ballot(take);
+    const int pos = n_u + __popcll(mk & ((1ull << lane) - 1ull));
+    if (take && pos < WAVE * UNION_PER_LANE) { sh.u.list.v[pos] = c.v; sh.u.list.id[pos] = c.id; }
+    n_u += __popcll(mk);
+  };
+  auto at_or_before_F = [&](const Cand<W>& c) {
+    const double d = double(c.v);
+    return d > F || (d == F && c.id <= F_id);
+  };
 #pragma unroll
   for (int r = 0; r < WAVE_BATCH; ++r) {
     const int idx = lane + WAVE * r;
-    const int sl = int((uint64_t(uint32_t(idx)) * inv_k) >> 20);
-    const double d = double(pre[r].v);
-    const bool take = idx < slots && idx - sl * k < sh.n_cand[min(sl, MAX_SLICES - 1)] &&
-                      (d > F || (d == F && pre[r].id <= F_id));
-    const uint64_t mk = __ballot(take);
-    const int pos = n_u + __popcll(mk & ((1ull << lane) - 1ull));
-    if (take && pos < WAVE * UNION_PER_LANE) { sh.u.list.v[pos] = pre[r].v; sh.u.list.id[pos] = pre[r].id; }
-    n_u += __popcll(mk);
+    const int sl = map.slice(idx);
+    add(idx < slices * pref && idx - sl * pref < sh.n_cand[min(sl, MAX_SLICES - 1)] && at_or_before_F(pre[r]), pre[r]);
+  }
+  // Candidates beyond the prefetch (a slice that stored more than `pref`).
+  const Cand<W>* cands = candidates<W>(a, row);
+  for (int sl = 0; sl < slices; ++sl) {
+    const int n_s = sh.n_cand[sl];
+    for (int base = pref; base < n_s; base += WAVE) {
+      const int i = base + lane;
+      Cand<W> c{};
+      if (i < n_s) c = fetch(cands + sl * cap + i);
+      add(i < n_s && at_or_before_F(c), c);
+    }
   }
   const int n_keep = p.top_k > 0 && p.top_k < valid_all ? int(p.top_k) : valid_all;
   if (n_u > WAVE * UNION_PER_LANE) return 0;
@@ -1621,6 +1657,21 @@ __device__ __forceinline__ int append_taken(const Visit& visit, uint64_t bits, S
   return sh.appended;
 }
 
+// Stores the tokens whose bits are set, in visit order, at out[0, popcount).
+template <class W, class Visit>
+__device__ __forceinline__ void publish_taken(const Visit& visit, uint64_t bits, Cand<W>* out) {
+  int o = 0;
+  visit([&](int i, int j, W x, int t) {
+    if ((bits >> (4 * i + j)) & 1ull) {
+      Cand<W> c{};
+      c.v = x;
+      c.id = t;
+      publish(out + o, c);
+      ++o;
+    }
+  });
+}
+
 // The slice's L-th valid token in (value desc, ID asc) order, given that at
 // least L valid tokens are >= floor: radix selection over the value's order
 // key among those tokens (8-bit digits), then the tie broken by ID, which is
@@ -1708,7 +1759,7 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
     const bool malformed = offsets_malformed(a);
     if (blockIdx.x == 0 && tid == 0) {
       reinterpret_cast<int32_t*>(a.workspace)[0] = malformed;
-      if (a.rows == 0) reinterpret_cast<uint32_t*>(a.workspace)[1] = 0;
+      reinterpret_cast<uint32_t*>(a.workspace)[1] = 0;
     }
     const int64_t req = int64_t(blockIdx.x) * BLOCK + tid;
     if (req < a.requests) {
@@ -1755,7 +1806,7 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
   Params p;
   slice_lookup(a, row, x0, x1, &p, sh);
   if (p.status != ES_OK) {
-    if (slice == 0) skip_row(a, row, sh);
+    if (slice == 0) skip_row(a, row);
     return;
   }
 
@@ -1789,17 +1840,10 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
     }
   }
   // What the candidate pass takes is decided by the request's scalars.
-  const int list_max = a.list_max;
-  int need = 0;  // 0: no candidates; > 0: the slice's top `need`; -1: all valid if they fit
-  if (p.temperature > 0 && list_max > 0 && !p.full_q) {
-    if (p.top_k >= 1 && p.top_k <= list_max) need = int(p.top_k);
-    else if (p.top_p < 1 && p.min_p == 0) need = TOPP_SLICE_NEED;
-    else need = -1;
-  }
-  const int L = need > 0 ? min(need, pl.cap_slice) : 0;
-  // Top-k rows with k <= 64 (and within the slice capacity) are finished by
-  // one wave of the merging block from sorted per-slice lists.
-  const bool sorted_list = need > 0 && L == need && need <= WAVE;
+  const ListPlan lp = list_plan(p, a.list_max, pl.cap_slice);
+  int need = lp.need;
+  const int L = lp.L;
+  const bool sorted_list = lp.sorted_list, need_topp = lp.need_topp;
   // The j-th largest thread maximum of the wave, j = ceil(L / 4): at least L
   // valid tokens of the slice are >= the smallest of the four waves' values.
   W tw = neg_inf<W>();
@@ -1843,40 +1887,35 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
   double frontier = -INFINITY, psum = 0, perr = 0;
   int n_cand = 0, pruned = 0, fid = INT_MAX;
   if (sorted_list && need > 0) {
-    // Top-k rows: the slice's first min(k, valid) tokens, sorted, for the merge wave.
+    // Top-k rows: every valid token >= the threshold (at least L of them),
+    // stored straight from the tile in any order; the merge wave selects.
+    // Complete down to (thr, every ID), or entirely when thr is -inf.
     const W thr = need < valid ? thr_all : neg_inf<W>();
     const W take_from = thr > W(-3.4028234663852886e38) ? thr : W(-3.4028234663852886e38);
-    int total = append_taken<W>(tile, collect_bits<W>(tile, [&](W x, int) { return x >= take_from; }), sh);
-    if (total > WAVE) {
+    Cand<W>* out = candidates<W>(a, row) + slice * pl.cap_slice;
+    const uint64_t bits = collect_bits<W>(tile, [&](W x, int) { return x >= take_from; });
+    const int mine = __popcll(bits);
+    const int slot = mine ? atomicAdd(&sh.appended, mine) : 0;
+    __syncthreads();
+    const int total = sh.appended;
+    if (total <= min(pl.cap_slice, WAVE)) {
+      if (mine) publish_taken<W>(tile, bits, out + slot);
+      n_cand = total;
+      frontier = double(thr);
+    } else {
       // Too many (ties, or a low threshold): exactly the first L instead.
       W cut_v;
       int cut_id;
       slice_cut<W, G>(mem, L, take_from, sh, &cut_v, &cut_id);
       if (tid == 0) sh.appended = 0;
       __syncthreads();
-      total = append_taken<W>(
-          mem, collect_bits<W>(mem, [&](W x, int t) { return x > cut_v || (x == cut_v && t <= cut_id); }), sh);
-    }
-    n_cand = min(total, L);
-    if (wave_id() == 0) {
-      const int n = min(total, WAVE);
-      W cv = neg_inf<W>();
-      int cid = INT_MAX;
-      if (lane < n) { cv = sh.u.list.v[lane]; cid = sh.u.list.id[lane]; }
-      const int rank = wave_rank(cv, cid, n);
-      if (lane < n && rank < n_cand) {
-        Cand<W> c{};
-        c.v = cv;
-        c.id = cid;
-        publish(candidates<W>(a, row) + slice * pl.cap_slice + rank, c);
-      }
-      // Complete down to the last stored token, or entirely.
-      const uint64_t last = __ballot(lane < n && rank == n_cand - 1);
-      if (valid > n_cand && last) {
-        const int src = __ffsll((unsigned long long)last) - 1;
-        frontier = double(lane_read(cv, src));
-        fid = lane_read(cid, src);
-      }
+      const uint64_t cb = collect_bits<W>(mem, [&](W x, int t) { return x > cut_v || (x == cut_v && t <= cut_id); });
+      const int cm = __popcll(cb);
+      const int cs = cm ? atomicAdd(&sh.appended, cm) : 0;
+      if (cm) publish_taken<W>(mem, cb, out + cs);
+      n_cand = L;
+      frontier = double(cut_v);
+      fid = cut_id;
     }
   } else if (need != 0) {
     const int cap = pl.cap_slice;
@@ -1927,7 +1966,7 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
       fid = -1;
     }
     // Top-p lists also need the kept weights' sum, relative to the slice maximum.
-    if (need == TOPP_SLICE_NEED && p.top_p < 1 && !(p.top_k >= 1 && p.top_k <= list_max)) {
+    if (need_topp) {
       const double ms = double(smax);
       const float inv_t = float(1.0 / p.temperature);
       const bool slow = !(inv_t < 1e30f);
@@ -1964,34 +2003,64 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
     part.n_cand = n_cand;
     part.pruned = pruned;
     part.flags = bad;
-    publish(slice_parts(a, row) + slice, part);
+    slice_parts(a, row)[slice] = part;
   }
-  if (!arrive(&counters(a, row)->slices, uint32_t(pl.slices), &sh.flag)) return;
+}
 
-  // ---- The last slice block merges the row. ----
-  // Wave 1 checks the request's per-row metadata while wave 0 fetches the
-  // slices' summaries (and a top-k row's sorted lists, every slot at once)
-  // and merges them in slice order.
+// ---------------------------------------------------------------------------
+// The finishing kernel: one block per row, after the slice pass (the kernel
+// boundary makes the slices' summaries and candidates visible). Wave 1 checks
+// the request's per-row metadata while wave 0 merges the slices in slice order
+// and, for a top-k row, finishes it; then the block routes the row: failed,
+// greedy, finished by the wave, the FP64 block list, or the full-row path
+// (reference: fused.cuh:803-933 prologue, :1250-1412 list, :1446-1810 full
+// row). The row is then committed (verify.cu:169-217 for drafted requests).
+template <int DT, bool VEC>
+__global__ void __launch_bounds__(BLOCK) es_finish(es_arguments a, Plan pl) {
+  using W = typename Ty<DT>::W;
+  __shared__ Shared<W> sh;
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  // Loads that depend on the row only come first: the offsets' first chunk,
+  // the slices' summaries and every candidate slot wave 0 may need.
+  int64_t x0 = 0, x1 = 0;
+  if (tid < a.requests) {
+    x0 = at(a.cu_rows, tid);
+    x1 = at(a.cu_rows, tid + 1);
+  }
+  const SlotMap map(min(pl.cap_slice, WAVE * WAVE_BATCH / pl.slices));
+  Cand<W> pre[WAVE_BATCH];
+  SlicePart q;
+  q.max_v = -INFINITY; q.second_v = -INFINITY; q.frontier = -INFINITY; q.tau = -INFINITY;
+  q.sum = 0; q.err = 0; q.max_id = INT_MAX; q.second_id = INT_MAX; q.valid = 0; q.n_cand = 0; q.pruned = 0; q.flags = 0;
+  if (wave_id() == 0) {
+    if (lane < pl.slices) q = slice_parts(a, row)[lane];
+    const Cand<W>* cands = candidates<W>(a, row);
+#pragma unroll
+    for (int r = 0; r < WAVE_BATCH; ++r) {
+      const int idx = lane + WAVE * r;
+      const int sl = map.slice(idx);
+      pre[r] = Cand<W>{};
+      if (idx < pl.slices * map.pref) pre[r] = cands[sl * pl.cap_slice + (idx - sl * map.pref)];
+    }
+  }
+  Params p;
+  slice_lookup(a, row, x0, x1, &p, sh);
+  if (p.status != ES_OK) {
+    // Malformed offsets or invalid request scalars: the request block reports it.
+    if (tid == 0) skip_row(a, row);
+    return;
+  }
+  const int list_max = a.list_max;
+  const ListPlan lp = list_plan(p, list_max, pl.cap_slice);
+  const bool sorted_list = lp.sorted_list, need_topp = lp.need_topp;
   load_row_rng(a, row, &p);
   if (wave_id() == 1) {
     const bool ok = request_rows_ok(a, p);
     if (lane == 0) sh.meta_bad = !ok;
   }
   if (wave_id() == 0) {
-    Cand<W> pre[WAVE_BATCH];
-    if (sorted_list) {
-      const Cand<W>* cands = candidates<W>(a, row);
-#pragma unroll
-      for (int r = 0; r < WAVE_BATCH; ++r) {
-        const int idx = lane + WAVE * r;
-        pre[r] = Cand<W>{};
-        if (idx < pl.slices * L) pre[r] = fetch(cands + (idx / L) * pl.cap_slice + idx % L);
-      }
-    }
-    SlicePart q;
-    q.max_v = -INFINITY; q.second_v = -INFINITY; q.frontier = -INFINITY; q.tau = -INFINITY;
-    q.sum = 0; q.err = 0; q.max_id = INT_MAX; q.second_id = INT_MAX; q.valid = 0; q.n_cand = 0; q.pruned = 0; q.flags = 0;
-    if (lane < pl.slices) q = fetch(slice_parts(a, row) + lane);
     if (lane < pl.slices) sh.n_cand[lane] = q.n_cand;
     struct T2d { double v1; int i1; double v2; int i2; };
     auto top2d = [](T2d x, T2d y) {
@@ -2013,17 +2082,21 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
                   Fr{-INFINITY, INT_MAX});
     const int nct = wave_all(q.n_cand, [](int x, int y) { return x + y; }, 0);
     // Top-p sums rescaled from slice maxima to the row maximum (FP64).
+    // (only top-p lists carry them: need == TOPP_SLICE_NEED in the slices).
     double s_sum = 0, s_err = 0;
-    int s_pr = q.pruned;
-    if (lane < pl.slices && q.valid > 0 && p.temperature > 0) {
-      const double shift = (t2.v1 - q.max_v) / p.temperature;
-      const double scale = exp(-shift);
-      if (shift > 700) { s_err = (q.sum + q.err) * scale + q.pruned * SUM_PRUNE_W; s_pr = 0; }
-      else { s_sum = q.sum * scale; s_err = (1.01 * q.err + 4.8e-7 * q.sum) * scale * (1 + 1e-14); }
+    int s_pr = 0;
+    if (need_topp) {
+      s_pr = q.pruned;
+      if (lane < pl.slices && q.valid > 0) {
+        const double shift = (t2.v1 - q.max_v) / p.temperature;
+        const double scale = exp(-shift);
+        if (shift > 700) { s_err = (q.sum + q.err) * scale + q.pruned * SUM_PRUNE_W; s_pr = 0; }
+        else { s_sum = q.sum * scale; s_err = (1.01 * q.err + 4.8e-7 * q.sum) * scale * (1 + 1e-14); }
+      }
+      s_sum = wave_all(s_sum, [](double x, double y) { return x + y; }, 0.0);
+      s_err = wave_all(s_err, [](double x, double y) { return x + y; }, 0.0);
+      s_pr = wave_all(s_pr, [](int x, int y) { return x + y; }, 0);
     }
-    s_sum = wave_all(s_sum, [](double x, double y) { return x + y; }, 0.0);
-    s_err = wave_all(s_err, [](double x, double y) { return x + y; }, 0.0);
-    s_pr = wave_all(s_pr, [](int x, int y) { return x + y; }, 0);
     if (lane == 0) {
       sh.maximum = t2.v1; sh.greedy = t2.i1; sh.runner_up = t2.v2; sh.runner_up_id = t2.i2;
       sh.valid = vsum; sh.bad = bsum; sh.frontier = fr.v; sh.frontier_id = fr.id; sh.n_cand_total = nct;
@@ -2035,7 +2108,7 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
     RowResult wr{0, 1, -1, -1, ES_OK, ES_OK};
     if (sorted_list && bsum == 0 && vsum > 0) {
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      wdone = wave_topk(a, row, p, sh, pre, pl.slices, pl.cap_slice, L, t2.v1, fr.v, fr.id, vsum, &wr);
+      wdone = wave_topk(a, row, p, sh, pre, map, pl.slices, pl.cap_slice, t2.v1, fr.v, fr.id, vsum, &wr);
     }
     if (lane == 0) {
       sh.wdone = wdone;
@@ -2045,7 +2118,7 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
   __syncthreads();
   if (sh.meta_bad) {
     // The request block reports the request as invalid.
-    skip_row(a, row, sh);
+    skip_row(a, row);
     return;
   }
   const int status = sh.bad ? ES_INVALID_INPUT : sh.valid == 0 ? ES_NO_VALID_TOKEN : ES_OK;
@@ -2086,37 +2159,21 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
       }
     }
     if (!done) {
-      // The full-row kernel finishes it; it arrives on the counters there.
-      if (tid == 0) {
-        RowState* st = row_state(a, row);
-        st->part = PART_FULL;
-        st->fallbacks = fallbacks;
-        st->route = 100 + why;  // why the list could not finish it (0: not a list row)
-      }
-      return;
+      // The full-row path: the row (and proposal row) read again as needed.
+      const double maximum = sh.maximum;
+      const int greedy = sh.greedy, runner_up_id = sh.runner_up_id, valid = sh.valid;
+      __syncthreads();
+      FullRow<DT, VEC> full(a, row, p, sh, pl.groups);
+      result = full.run(maximum, greedy, runner_up_id, valid);
+      result.target_status = ES_OK;
+      fallbacks += full.fallbacks;
+      route = 100 + why;  // why the list could not finish it (0: not a list row)
     }
   }
   complete_row(a, row, p, result, fallbacks, route, sh);
+  if (tid == 0) add_fallbacks(a, unsigned(fallbacks));
 }
 
-// ---------------------------------------------------------------------------
-// The full-row kernel: one block per row marked PART_FULL by es_main; every
-// other block returns at once.
-template <int DT, bool VEC>
-__global__ void __launch_bounds__(BLOCK) es_full(es_arguments a, Plan pl) {
-  using W = typename Ty<DT>::W;
-  __shared__ Shared<W> sh;
-  __shared__ Params sp;
-  const int64_t row = blockIdx.x;
-  const RowState st = *row_state(a, row);
-  if (st.part != PART_FULL) return;
-  block_params(a, row, &sp, sh);
-  const Params p = sp;
-  FullRow<DT, VEC> full(a, row, p, sh, pl.groups);
-  RowResult result = full.run(st.maximum, st.greedy, st.runner_up_id, st.valid);
-  result.target_status = ES_OK;
-  complete_row(a, row, p, result, st.fallbacks + full.fallbacks, st.route, sh);
-}
 
 }  // namespace es
 
@@ -2130,7 +2187,7 @@ hipError_t launch_main(const es_arguments& a, const Plan& pl, hipStream_t stream
   hipLaunchKernelGGL((es_main<DT, VEC, G>), dim3(blocks), dim3(BLOCK), 0, stream, a, pl);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || a.rows == 0) return err;
-  hipLaunchKernelGGL((es_full<DT, VEC>), dim3(unsigned(a.rows)), dim3(BLOCK), 0, stream, a, pl);
+  hipLaunchKernelGGL((es_finish<DT, VEC>), dim3(unsigned(a.rows)), dim3(BLOCK), 0, stream, a, pl);
   return hipGetLastError();
 }
 
