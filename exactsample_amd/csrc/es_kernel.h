@@ -285,7 +285,6 @@ template <class W> struct Shared {
   W st_max[WAVES], st_thr[WAVES];
   int st_id[WAVES], st_valid[WAVES], st_bad[WAVES];
   int appended;
-  int meta_bad;
   // The merge wave's decision, broadcast to the block.
   RowResult wres;
   int wroute, wfallbacks, wdone;
@@ -296,10 +295,15 @@ struct Params {
   int64_t req, begin, end;
   double temperature, top_p, min_p;
   int64_t top_k;
-  int32_t status;
+  int32_t status;    // ES_INVALID_INPUT for malformed offsets or invalid request scalars
+  int32_t meta_bad;  // a position or draft ID of the request out of range
   int draft_row, verify, coupled, full_q, draft_id;
   RngAddr rng;
 };
+static_assert(sizeof(Params) <= ROW_META_BYTES, "Params fits the row's meta area");
+__device__ __forceinline__ Params* row_meta(const es_arguments& a, int64_t row) {
+  return reinterpret_cast<Params*>(row_region(a, row) + OFF_META);
+}
 
 // The row's request and its parameters, checked by the whole block: the
 // offsets are scanned once (malformed check and owner lookup together) and the
@@ -408,6 +412,7 @@ __device__ __forceinline__ void slice_lookup(const es_arguments& a, int64_t row,
   }
   req = __builtin_amdgcn_readfirstlane(req);
   p->status = ES_OK;
+  p->meta_bad = 0;
   if (malformed || req < 0 || end - begin > a.max_draft + 1) {
     p->status = ES_INVALID_INPUT;
     return;
@@ -1593,11 +1598,13 @@ template <int DT, bool VEC> struct FullRow {
 template <class W, int G> struct TileVisit {
   const W (&v)[G][4];
   int gb;
+  uint64_t allow;  // tokens of the tile in the slice and allowed by the mask
   template <class F> __device__ __forceinline__ void operator()(F&& f) const {
 #pragma unroll
     for (int i = 0; i < G; ++i) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) f(i, j, v[i][j], 4 * (gb + BLOCK * i) + j);
+      for (int j = 0; j < 4; ++j)
+        f(i, j, ((allow >> (4 * i + j)) & 1ull) ? v[i][j] : neg_inf<W>(), 4 * (gb + BLOCK * i) + j);
     }
   }
 };
@@ -1779,110 +1786,159 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
 
   // The first chunk of the offsets, then the tile: waiting for the offsets
   // (vmcnt counts loads in issue order) leaves the tile loads in flight. Every
-  // lane loads the tile (an index clamped into the row), so there is no branch
-  // per load; tokens outside the slice are then set to -inf.
+  // lane loads the whole tile (indexes clamped into the slice), so there is no
+  // branch per load.
   int64_t x0 = 0, x1 = 0;
   if (tid < a.requests) {
     x0 = at(a.cu_rows, tid);
     x1 = at(a.cu_rows, tid + 1);
   }
   __builtin_amdgcn_sched_barrier(0);
+  // Tile loads. Groups past the slice's end are loaded as copies of its last
+  // group: they never change the maximum or the checks below, and `allow`
+  // keeps them out of counts and candidates.
   W v[G][4];
-  uint64_t mbits = ~0ull;
   const int gb = g0 + tid;
 #pragma unroll
-  for (int i = 0; i < G; ++i) view.load(min(gb + BLOCK * i, pl.groups - 1), v[i]);
+  for (int i = 0; i < G; ++i) view.load(min(gb + BLOCK * i, g1 - 1), v[i]);
+  const int n_in = g1 > gb ? min(G, (g1 - gb + BLOCK - 1) / BLOCK) : 0;  // groups of the tile in the slice
+  uint64_t allow = 4 * n_in >= 64 ? ~0ull : (1ull << (4 * n_in)) - 1ull;
   if (a.mask) {
-    mbits = 0;
+    uint64_t mbits = 0;
+    const int32_t* mrow = a.mask + row * a.mask_s0;
 #pragma unroll
-    for (int i = 0; i < G; ++i) mbits |= uint64_t(group_bits(a, row, min(gb + BLOCK * i, pl.groups - 1))) << (4 * i);
-  }
-#pragma unroll
-  for (int i = 0; i < G; ++i) {
-    const bool in = gb + BLOCK * i < g1;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[i][j] = in ? v[i][j] : neg_inf<W>();
+    for (int i = 0; i < G; ++i) {
+      const int g = min(gb + BLOCK * i, g1 - 1);
+      mbits |= uint64_t((uint32_t(mrow[int64_t((4 * g) >> 5) * a.mask_s1]) >> ((4 * g) & 31)) & 0xfu) << (4 * i);
+    }
+    allow &= mbits;
   }
   Params p;
   slice_lookup(a, row, x0, x1, &p, sh);
-  if (p.status != ES_OK) {
-    if (slice == 0) skip_row(a, row);
-    return;
-  }
-
-  // ---- Statistics: NaN/+inf anywhere (even masked), valid count, maximum. ----
-  int bad_l = 0, valid_l = 0;
-  W mx = neg_inf<W>();
-#pragma unroll
-  for (int i = 0; i < G; ++i) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) bad_l |= isnan(v[i][j]) || v[i][j] == W(INFINITY);
-  }
-  // Unconditional (mbits is all ones without a mask): a branch here would keep
-  // a masked and an unmasked copy of the tile alive at its join.
-#pragma unroll
-  for (int i = 0; i < G; ++i) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[i][j] = ((mbits >> (4 * i + j)) & 1ull) ? v[i][j] : neg_inf<W>();
-  }
-  // From here on a token is valid exactly when its value is above -inf (a NaN
-  // token only occurs in an invalid row, whose other results are unused). The
-  // thread's maximum keeps its lowest ID: IDs rise with (i, j).
-  int fid_l = INT_MAX;
-#pragma unroll
-  for (int i = 0; i < G; ++i) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      valid_l += v[i][j] > neg_inf<W>();
-      const bool up = v[i][j] > mx;
-      fid_l = up ? 4 * (gb + BLOCK * i) + j : fid_l;
-      mx = up ? v[i][j] : mx;
+  if (slice == 0 && wave_id() == 0) {
+    // The row's first slice records what the finishing block needs: the
+    // request's parameters, its per-row metadata check and the RNG address.
+    if (p.status == ES_OK) {
+      load_row_rng(a, row, &p);
+      p.meta_bad = !request_rows_ok(a, p);
     }
+    if (lane == 0) *row_meta(a, row) = p;
   }
-  // What the candidate pass takes is decided by the request's scalars.
+  if (p.status != ES_OK) return;
   const ListPlan lp = list_plan(p, a.list_max, pl.cap_slice);
   int need = lp.need;
   const int L = lp.L;
   const bool sorted_list = lp.sorted_list, need_topp = lp.need_topp;
-  // The j-th largest thread maximum of the wave, j = ceil(L / 4): at least L
-  // valid tokens of the slice are >= the smallest of the four waves' values.
-  W tw = neg_inf<W>();
-  if (L > 0) tw = key_value(wave_kth_largest(order_key(mx), (L + WAVES - 1) / WAVES));
-  // One exchange between the waves: counts, flags, the maximum with its
-  // lowest ID and the thresholds.
-  const int valid_w = wave_all(valid_l, [](int x, int y) { return x + y; }, 0);
-  const int bad_w = __ballot(bad_l) != 0;
-  struct MI { W v; int id; };
-  const MI wm = wave_all(MI{mx, fid_l}, [](MI x, MI y) { return (y.v > x.v || (y.v == x.v && y.id < x.id)) ? y : x; },
-                         MI{neg_inf<W>(), INT_MAX});
-  const W wmax = wm.v;
-  const int wid = wm.id;
-  if (lane == 0) {
-    sh.st_max[wave_id()] = wmax;
-    sh.st_id[wave_id()] = wid;
-    sh.st_valid[wave_id()] = valid_w;
-    sh.st_bad[wave_id()] = bad_w;
-    sh.st_thr[wave_id()] = tw;
+  const int j_thr = (L + WAVES - 1) / WAVES;  // thread maxima per wave behind the candidate threshold
+
+  // ---- Statistics (reference: fused.cuh:409-519 row_stats). ----
+  // Fast pass: the maximum over the slice's tokens (the candidate threshold
+  // counts distinct tokens through it, so copies are left out) and a
+  // non-finite detector over the tile (x * 0 is NaN exactly when x is NaN or
+  // infinite).
+  W mx = neg_inf<W>(), nf = W(0);
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const bool in = i < n_in;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      mx = in && v[i][j] > mx ? v[i][j] : mx;
+      nf = nf + v[i][j] * W(0);
+    }
+  }
+  // The wave's maximum and its lowest ID (IDs rise with (i, thread, j)).
+  auto wave_max_id = [&](W m, uint64_t ok_bits) {
+    struct MI { W v; int id; };
+    const W wmax = wave_all(m, [](W x, W y) { return x > y ? x : y; }, neg_inf<W>());
+    int id = INT_MAX;
+    if (m == wmax && wmax > neg_inf<W>()) {
+#pragma unroll
+      for (int i = G - 1; i >= 0; --i) {
+#pragma unroll
+        for (int j = 3; j >= 0; --j)
+          if (((ok_bits >> (4 * i + j)) & 1ull) && v[i][j] == wmax) id = 4 * (gb + BLOCK * i) + j;
+      }
+    }
+    return MI{wmax, wave_all(id, [](int x, int y) { return x < y ? x : y; }, INT_MAX)};
+  };
+  {
+    const auto wm = wave_max_id(mx, 4 * n_in >= 64 ? ~0ull : (1ull << (4 * n_in)) - 1ull);
+    const W tw = L > 0 ? key_value(wave_kth_largest(order_key(mx), j_thr)) : neg_inf<W>();
+    const int nonfinite_w = __ballot(!(nf == W(0))) != 0;
+    if (lane == 0) {
+      sh.st_max[wave_id()] = wm.v;
+      sh.st_id[wave_id()] = wm.id;
+      sh.st_bad[wave_id()] = nonfinite_w;
+      sh.st_thr[wave_id()] = tw;
+    }
   }
   if (tid == 0) sh.appended = 0;
   __syncthreads();
-  int valid = 0, bad = 0, first_id = INT_MAX;
+  int valid = 4 * (g1 - g0), bad = 0, first_id = INT_MAX, special = 0;
   W smax = neg_inf<W>(), thr_all = W(INFINITY);
+  auto combine = [&]() {
 #pragma unroll
-  for (int w = 0; w < WAVES; ++w) {
-    valid += sh.st_valid[w];
-    bad |= sh.st_bad[w];
-    if (sh.st_max[w] > smax || (sh.st_max[w] == smax && sh.st_id[w] < first_id)) {
-      smax = sh.st_max[w];
-      first_id = sh.st_id[w];
+    for (int w = 0; w < WAVES; ++w) {
+      if (sh.st_max[w] > smax || (sh.st_max[w] == smax && sh.st_id[w] < first_id)) {
+        smax = sh.st_max[w];
+        first_id = sh.st_id[w];
+      }
+      thr_all = sh.st_thr[w] < thr_all ? sh.st_thr[w] : thr_all;
     }
-    thr_all = sh.st_thr[w] < thr_all ? sh.st_thr[w] : thr_all;
+  };
+  combine();
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) special |= sh.st_bad[w];
+  if (special || a.mask || !VEC) {
+    // Exact pass: a non-finite value, a mask or element loads. NaN/+inf
+    // anywhere (even masked) makes the row invalid; valid tokens are the
+    // allowed ones above -inf.
+    int bad_l = 0, valid_l = 0, fid_l = INT_MAX;
+    W m2 = neg_inf<W>();
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const W x = v[i][j];
+        bad_l |= x != x || x == W(INFINITY);
+        const bool ok = ((allow >> (4 * i + j)) & 1ull) && x > neg_inf<W>();
+        valid_l += ok;
+        const bool up = ok && x > m2;
+        fid_l = up ? 4 * (gb + BLOCK * i) + j : fid_l;
+        m2 = up ? x : m2;
+      }
+    }
+    struct MI { W v; int id; };
+    const MI wm = wave_all(MI{m2, fid_l}, [](MI x, MI y) { return (y.v > x.v || (y.v == x.v && y.id < x.id)) ? y : x; },
+                           MI{neg_inf<W>(), INT_MAX});
+    const W tw = L > 0 ? key_value(wave_kth_largest(order_key(m2), j_thr)) : neg_inf<W>();
+    const int valid_w = wave_all(valid_l, [](int x, int y) { return x + y; }, 0);
+    const int bad_w = __ballot(bad_l) != 0;
+    __syncthreads();
+    if (lane == 0) {
+      sh.st_max[wave_id()] = wm.v;
+      sh.st_id[wave_id()] = wm.id;
+      sh.st_valid[wave_id()] = valid_w;
+      sh.st_bad[wave_id()] = bad_w;
+      sh.st_thr[wave_id()] = tw;
+    }
+    __syncthreads();
+    valid = 0;
+    first_id = INT_MAX;
+    smax = neg_inf<W>();
+    thr_all = W(INFINITY);
+    combine();
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      valid += sh.st_valid[w];
+      bad |= sh.st_bad[w];
+    }
   }
   if (bad) need = 0;
 
   // ---- Candidates for a list row. ----
   // The tile serves the first selection; anything after it re-reads memory.
-  const TileVisit<W, G> tile{v, gb};
+  const TileVisit<W, G> tile{v, gb, allow};
   const MemVisit<DT, VEC, G> mem(a, row, view, gb, g1, pl.groups);
   double frontier = -INFINITY, psum = 0, perr = 0;
   int n_cand = 0, pruned = 0, fid = INT_MAX;
@@ -2022,13 +2078,9 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments a, Plan pl) {
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = lane_id();
-  // Loads that depend on the row only come first: the offsets' first chunk,
-  // the slices' summaries and every candidate slot wave 0 may need.
-  int64_t x0 = 0, x1 = 0;
-  if (tid < a.requests) {
-    x0 = at(a.cu_rows, tid);
-    x1 = at(a.cu_rows, tid + 1);
-  }
+  // One round of loads: the row's parameters (recorded by its first slice
+  // block), the slices' summaries and every candidate slot wave 0 may need.
+  const Params p = *row_meta(a, row);
   const SlotMap map(min(pl.cap_slice, WAVE * WAVE_BATCH / pl.slices));
   Cand<W> pre[WAVE_BATCH];
   SlicePart q;
@@ -2045,21 +2097,14 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments a, Plan pl) {
       if (idx < pl.slices * map.pref) pre[r] = cands[sl * pl.cap_slice + (idx - sl * map.pref)];
     }
   }
-  Params p;
-  slice_lookup(a, row, x0, x1, &p, sh);
-  if (p.status != ES_OK) {
-    // Malformed offsets or invalid request scalars: the request block reports it.
-    if (tid == 0) skip_row(a, row);
+  if (p.status != ES_OK || p.meta_bad) {
+    // Malformed offsets or invalid request metadata: the request block reports it.
+    skip_row(a, row);
     return;
   }
   const int list_max = a.list_max;
   const ListPlan lp = list_plan(p, list_max, pl.cap_slice);
   const bool sorted_list = lp.sorted_list, need_topp = lp.need_topp;
-  load_row_rng(a, row, &p);
-  if (wave_id() == 1) {
-    const bool ok = request_rows_ok(a, p);
-    if (lane == 0) sh.meta_bad = !ok;
-  }
   if (wave_id() == 0) {
     if (lane < pl.slices) sh.n_cand[lane] = q.n_cand;
     struct T2d { double v1; int i1; double v2; int i2; };
@@ -2116,11 +2161,6 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments a, Plan pl) {
     }
   }
   __syncthreads();
-  if (sh.meta_bad) {
-    // The request block reports the request as invalid.
-    skip_row(a, row);
-    return;
-  }
   const int status = sh.bad ? ES_INVALID_INPUT : sh.valid == 0 ? ES_NO_VALID_TOKEN : ES_OK;
   if (tid == 0) {
     RowState* st = row_state(a, row);

@@ -3,7 +3,8 @@
 //
 //   [0, 8)            header: int32 malformed-offsets flag, uint32 fallback count
 //   8 + r * ROW_BYTES row r's region (ROW_BYTES = 12320, the reference's
-//                     32 B RowResult + 12288 B scratch per row, api.h:37-43)
+//                     32 B RowResult + 12288 B scratch per row, api.h:37-43):
+//                     result, state, counters, meta, slice parts, candidates
 //
 // A row's region sits at a fixed address whatever the call's row count, so the
 // arrival counters inside it stay where the previous call left them (zero):
@@ -67,10 +68,15 @@ struct SlicePart {
 };
 static_assert(sizeof(SlicePart) == 72, "SlicePart layout");
 
+// The row's request parameters as the slice pass resolved them (written by
+// the row's first slice block, read by the finishing block).
+constexpr size_t ROW_META_BYTES = 128;
+
 constexpr size_t OFF_RESULT = 0;
 constexpr size_t OFF_STATE = OFF_RESULT + ROW_RESULT_BYTES;
 constexpr size_t OFF_COUNTERS = OFF_STATE + sizeof(RowState);
-constexpr size_t OFF_PARTS = OFF_COUNTERS + sizeof(Counters);
+constexpr size_t OFF_META = OFF_COUNTERS + sizeof(Counters);
+constexpr size_t OFF_PARTS = OFF_META + ROW_META_BYTES;
 constexpr size_t OFF_CAND = OFF_PARTS + MAX_SLICES * sizeof(SlicePart);
 constexpr size_t CAND_BYTES = ROW_BYTES - OFF_CAND;
 static_assert(OFF_CAND % 16 == 0, "candidate area alignment");
