@@ -106,7 +106,7 @@ int32_t es_launch(const es_arguments* args, void* stream_ptr) {
     pl.gps = int(groups);
   } else {
     pl.slices = geo.slices;
-    pl.gps = int((groups + geo.slices - 1) / geo.slices);
+    pl.gps = geo.g * kBlock;  // every slice but the last is exactly one tile
   }
   const int cap_total = a.target.dtype == ES_F64 ? es::cand_capacity<double>() : es::cand_capacity<float>();
   pl.cap_slice = cap_total / pl.slices;

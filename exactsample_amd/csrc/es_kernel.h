@@ -964,33 +964,49 @@ __device__ __forceinline__ int wave_topk(const es_arguments& a, int64_t row, con
   if (n_u > WAVE * UNION_PER_LANE) return 0;
   if (n_u < n_keep || n_keep < 1) return -1;  // cannot happen for a complete union
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  // The n_keep-th largest value of the union: its order key, bit by bit.
+  // Bins of the union by distance below the row maximum (quarter logits, the
+  // last bin for 63.75 and more): monotone in the order, so the bins up to the
+  // one holding the n_keep-th entry hold a prefix of the order (the pool).
+  unsigned* bins = reinterpret_cast<unsigned*>(sh.u.list.sid);  // HEAD_BINS counters
+#pragma unroll
+  for (int r = 0; r < HEAD_BINS / WAVE; ++r) bins[lane + WAVE * r] = 0;
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   const int per = (n_u + WAVE - 1) / WAVE;
-  K key[UNION_PER_LANE];
+  int bin_of[UNION_PER_LANE];
 #pragma unroll
   for (int r = 0; r < UNION_PER_LANE; ++r) {
     const int idx = lane + WAVE * r;
-    key[r] = r < per && idx < n_u ? order_key(sh.u.list.v[idx]) : K(0);
+    bin_of[r] = HEAD_BINS;
+    if (r < per && idx < n_u) {
+      bin_of[r] = head_bin(M - double(sh.u.list.v[idx]));
+      atomicAdd(&bins[bin_of[r]], 1u);
+    }
   }
-  K prefix = 0;
-  for (int b = int(sizeof(K) * 8) - 1; b >= 0; --b) {
-    const K cand = prefix | (K(1) << b);
-    int count = 0;
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  // Lane l owns bins [4l, 4l + 4): the first bin whose running total reaches n_keep.
+  constexpr int BPL = HEAD_BINS / WAVE;
+  unsigned bc[BPL], local = 0;
 #pragma unroll
-    for (int r = 0; r < UNION_PER_LANE; ++r)
-      if (r < per) count += __popcll(__ballot(key[r] >= cand));
-    if (count >= n_keep) prefix = cand;
+  for (int q = 0; q < BPL; ++q) { bc[q] = bins[BPL * lane + q]; local += bc[q]; }
+  const unsigned incl_b = wave_scan_add(local);
+  int mine_cut = INT_MAX;
+  unsigned run = incl_b - local;
+#pragma unroll
+  for (int q = 0; q < BPL; ++q) {
+    run += bc[q];
+    if (mine_cut == INT_MAX && run >= unsigned(n_keep)) mine_cut = BPL * lane + q;
   }
-  // The pool: union entries >= that value, one per lane.
+  const int cut_bin = wave_all(mine_cut, [](int x, int y) { return x < y ? x : y; }, INT_MAX);
+  // The pool: union entries in bins up to cut_bin, one per lane.
   int n_pool = 0;
 #pragma unroll
   for (int r = 0; r < UNION_PER_LANE; ++r) {
     if (r >= per) break;
     const int idx = lane + WAVE * r;
-    const bool take = idx < n_u && key[r] >= prefix;
+    const bool take = idx < n_u && bin_of[r] <= cut_bin;
     const uint64_t mk = __ballot(take);
     const int pos = n_pool + __popcll(mk & ((1ull << lane) - 1ull));
-    if (take && pos < WAVE) { sh.u.list.sv[pos] = sh.u.list.v[idx]; sh.u.list.sid[pos] = sh.u.list.id[idx]; }
+    if (take && pos < WAVE) { sh.u.list.sv[pos] = sh.u.list.v[idx]; sh.u.list.w[pos] = double(sh.u.list.id[idx]); }
     n_pool += __popcll(mk);
   }
   if (n_pool > WAVE) return 0;  // a wide tie at the k-th value
@@ -998,7 +1014,7 @@ __device__ __forceinline__ int wave_topk(const es_arguments& a, int64_t row, con
   // Rank sort of the pool, one entry per lane.
   W v = neg_inf<W>();
   int id = INT_MAX;
-  if (lane < n_pool) { v = sh.u.list.sv[lane]; id = sh.u.list.sid[lane]; }
+  if (lane < n_pool) { v = sh.u.list.sv[lane]; id = int(sh.u.list.w[lane]); }
   const int rank = wave_rank(v, id, n_pool);
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   if (lane < n_pool) { sh.u.list.v[rank] = v; sh.u.list.id[rank] = id; }
@@ -1689,7 +1705,7 @@ __device__ __forceinline__ void slice_cut(const Visit& visit, int L, W floor, Sh
   constexpr int KB = int(sizeof(K) * 8);
   // Scratch in the block's union: 256 counters, then G x BLOCK tie counts.
   unsigned* hist = reinterpret_cast<unsigned*>(&sh.u);
-  static_assert(sizeof(sh.u) >= (256 + G * BLOCK) * sizeof(int), "slice_cut scratch");
+  static_assert(sizeof(sh.u) >= (256 + G * BLOCK + WAVES * G) * sizeof(int), "slice_cut scratch");
   K prefix = 0, known = 0;
   int need = L;
   for (int shift = KB - 8; shift >= 0; shift -= 8) {
@@ -1713,33 +1729,35 @@ __device__ __forceinline__ void slice_cut(const Visit& visit, int L, W floor, Sh
     known |= K(255) << shift;
   }
   const W cut_v = key_value(prefix);
-  // `need` tokens with value cut_v are taken, the lowest IDs first.
+  // `need` tokens with value cut_v are taken, the lowest IDs first. IDs rise
+  // with (i, thread, j): the per-(i, thread) tie counts locate the group row
+  // i holding the need-th tie (totals over threads per i), then the thread
+  // (a scan over threads at that i), then the tie inside the thread's group.
   int* ties = reinterpret_cast<int*>(&sh.u) + 256;  // [G][BLOCK]
   for (int i = 0; i < G; ++i) ties[i * BLOCK + threadIdx.x] = 0;
   visit([&](int i, int, W x, int) { ties[i * BLOCK + threadIdx.x] += x == cut_v; });
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int before = 0, gi = 0;
-    for (; gi < G; ++gi) {
-      int s = 0;
-      for (int t = 0; t < BLOCK; ++t) s += ties[gi * BLOCK + t];
-      if (before + s >= need) break;
-      before += s;
-    }
-    int t = 0;
-    for (; t < BLOCK; ++t) {
-      const int c = ties[gi * BLOCK + t];
-      if (before + c >= need) break;
-      before += c;
-    }
-    sh.pick = gi;
-    sh.n = t;
-    sh.flag = need - before;  // the rank of the last taken tie inside that thread's group
+  int* row_tot = reinterpret_cast<int*>(&sh.u) + 256 + G * BLOCK;  // [WAVES][G]
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int t = wave_all(ties[i * BLOCK + threadIdx.x], [](int x, int y) { return x + y; }, 0);
+    if (lane_id() == 0) row_tot[wave_id() * G + i] = t;
   }
+  if (threadIdx.x == 0) sh.ck = INT_MAX;
   __syncthreads();
-  const int gi = sh.pick, owner = sh.n, rank = sh.flag;
-  __syncthreads();
-  if (int(threadIdx.x) == owner) {
+  int gi = 0, before = 0;
+  for (; gi < G; ++gi) {
+    int t = 0;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) t += row_tot[w * G + gi];
+    if (before + t >= need) break;
+    before += t;
+  }
+  gi = min(gi, G - 1);
+  const int c = ties[gi * BLOCK + threadIdx.x];
+  int all;
+  const int incl = block_scan_add(c, sh.ired, &all) + before;
+  if (c > 0 && incl >= need && incl - c < need) {
+    const int rank = need - (incl - c);  // the rank of the last taken tie inside this thread's group
     int seen = 0, id = INT_MAX;
     visit([&](int i, int, W x, int t) {
       if (i == gi && x == cut_v && ++seen == rank) id = t;
@@ -1832,19 +1850,21 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
   const int j_thr = (L + WAVES - 1) / WAVES;  // thread maxima per wave behind the candidate threshold
 
   // ---- Statistics (reference: fused.cuh:409-519 row_stats). ----
-  // Fast pass: the maximum over the slice's tokens (the candidate threshold
-  // counts distinct tokens through it, so copies are left out) and a
-  // non-finite detector over the tile (x * 0 is NaN exactly when x is NaN or
-  // infinite).
+  // Fast pass: per-group maxima, the slice's maximum over its own groups (the
+  // candidate threshold counts distinct tokens through it, so the copies past
+  // the slice's end are left out) and a non-finite detector over the tile
+  // (fma(x, 0, acc) turns NaN for a NaN or infinite x and stays so).
+  auto group_max = [&](int i) {
+    const W m01 = v[i][0] > v[i][1] ? v[i][0] : v[i][1], m23 = v[i][2] > v[i][3] ? v[i][2] : v[i][3];
+    return m01 > m23 ? m01 : m23;
+  };
   W mx = neg_inf<W>(), nf = W(0);
 #pragma unroll
   for (int i = 0; i < G; ++i) {
-    const bool in = i < n_in;
+    const W gmi = group_max(i);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      mx = in && v[i][j] > mx ? v[i][j] : mx;
-      nf = nf + v[i][j] * W(0);
-    }
+    for (int j = 0; j < 4; ++j) nf = fma(v[i][j], W(0), nf);
+    mx = i < n_in && gmi > mx ? gmi : mx;
   }
   // The wave's maximum and its lowest ID (IDs rise with (i, thread, j)).
   auto wave_max_id = [&](W m, uint64_t ok_bits) {
@@ -1892,7 +1912,7 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
   if (special || a.mask || !VEC) {
     // Exact pass: a non-finite value, a mask or element loads. NaN/+inf
     // anywhere (even masked) makes the row invalid; valid tokens are the
-    // allowed ones above -inf.
+    // allowed ones above -inf, and the group maxima are taken over them.
     int bad_l = 0, valid_l = 0, fid_l = INT_MAX;
     W m2 = neg_inf<W>();
 #pragma unroll
@@ -1945,17 +1965,43 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
   if (sorted_list && need > 0) {
     // Top-k rows: every valid token >= the threshold (at least L of them),
     // stored straight from the tile in any order; the merge wave selects.
-    // Complete down to (thr, every ID), or entirely when thr is -inf.
+    // Complete down to (thr, every ID), or entirely when thr is -inf. Only
+    // groups whose maximum reaches the threshold are looked into.
     const W thr = need < valid ? thr_all : neg_inf<W>();
     const W take_from = thr > W(-3.4028234663852886e38) ? thr : W(-3.4028234663852886e38);
     Cand<W>* out = candidates<W>(a, row) + slice * pl.cap_slice;
-    const uint64_t bits = collect_bits<W>(tile, [&](W x, int) { return x >= take_from; });
-    const int mine = __popcll(bits);
-    const int slot = mine ? atomicAdd(&sh.appended, mine) : 0;
+    // A group may hold a candidate when it is in the slice and its maximum
+    // reaches the threshold (masked tokens are excluded token by token). Its
+    // candidates take slots from an LDS counter and are stored at once; slots
+    // past the list's capacity are not written (the exact cut below then
+    // rewrites the list).
+    const int limit = pl.cap_slice;
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      if (i < n_in && group_max(i) >= take_from) {
+        int cnt = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) cnt += ((allow >> (4 * i + j)) & 1ull) && v[i][j] >= take_from;
+        if (cnt) {
+          int o = atomicAdd(&sh.appended, cnt);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if (((allow >> (4 * i + j)) & 1ull) && v[i][j] >= take_from) {
+              if (o < limit) {
+                Cand<W> c{};
+                c.v = v[i][j];
+                c.id = 4 * (gb + BLOCK * i) + j;
+                out[o] = c;
+              }
+              ++o;
+            }
+          }
+        }
+      }
+    }
     __syncthreads();
     const int total = sh.appended;
-    if (total <= min(pl.cap_slice, WAVE)) {
-      if (mine) publish_taken<W>(tile, bits, out + slot);
+    if (total <= limit) {
       n_cand = total;
       frontier = double(thr);
     } else {
