@@ -931,12 +931,15 @@ __device__ __forceinline__ int wave_topk(const es_arguments& a, int64_t row, con
   using K = typename std::conditional<sizeof(W) == 8, uint64_t, uint32_t>::type;
   const int lane = lane_id();
   const int pref = map.pref;
-  // The union at or before F, compacted into LDS.
-  int n_u = 0;
+  // The union at or before F, compacted into LDS. The row's greedy token (the
+  // lowest ID holding the maximum M) is among it: every slice stored its
+  // tokens at its own maximum.
+  int n_u = 0, greedy = INT_MAX;
   auto add = [&](bool take, const Cand<W>& c) {
     const uint64_t mk = __ballot(take);
     const int pos = n_u + __popcll(mk & ((1ull << lane) - 1ull));
     if (take && pos < WAVE * UNION_PER_LANE) { sh.u.list.v[pos] = c.v; sh.u.list.id[pos] = c.id; }
+    if (take && double(c.v) == M && c.id < greedy) greedy = c.id;
     n_u += __popcll(mk);
   };
   auto at_or_before_F = [&](const Cand<W>& c) {
@@ -960,6 +963,8 @@ __device__ __forceinline__ int wave_topk(const es_arguments& a, int64_t row, con
       add(i < n_s && at_or_before_F(c), c);
     }
   }
+  greedy = wave_all(greedy, [](int x, int y) { return x < y ? x : y; }, INT_MAX);
+  if (lane == 0) sh.greedy = greedy;
   const int n_keep = p.top_k > 0 && p.top_k < valid_all ? int(p.top_k) : valid_all;
   if (n_u > WAVE * UNION_PER_LANE) return 0;
   if (n_u < n_keep || n_keep < 1) return -1;  // cannot happen for a complete union
@@ -1517,7 +1522,7 @@ template <int DT, bool VEC> struct FullRow {
     }
     auto in_final = [&](int t, W v, bool ok) { return in_k(t, v, ok) && CK<W>::make(v, t) >= cut; };
     // The floor of a draw: the first token of the order that the draw may take.
-    const int floor_token = greedy;
+    const int floor_token = greedy >= 0 && greedy < int(a.vocab) ? greedy : -1;
     // ---- Ratio test (reference.py:229-230). ----
     if (p.verify) {
       const W vx = view.value(p.draft_id);
@@ -1563,7 +1568,7 @@ template <int DT, bool VEC> struct FullRow {
       if (accept) return r;
       if (!full_q) {
         const int floor_id = p.draft_id == greedy ? (runner_up_id != INT_MAX ? runner_up_id : -1) : greedy;
-        int fl = floor_id;
+        int fl = floor_id >= 0 && floor_id < int(a.vocab) ? floor_id : -1;
         if (fl >= 0 && fl != greedy) {
           const W vf = view.value(fl);
           if (!in_final(fl, vf, allowed(a, row, fl))) fl = -1;
@@ -1607,24 +1612,9 @@ template <int DT, bool VEC> struct FullRow {
 // ---------------------------------------------------------------------------
 // The slice's tokens in the register tile's order. Token (i, j) of a thread
 // is 4 * (gb + BLOCK * i) + j, so IDs rise with (i, thread, j); tokens that
-// are masked or outside the slice have the value -inf. TileVisit walks the
-// tile in registers; MemVisit reads the same tokens again from memory, for the
-// rare paths that run after the tile is gone (so the tile's registers are not
-// held through them).
-template <class W, int G> struct TileVisit {
-  const W (&v)[G][4];
-  int gb;
-  uint64_t allow;  // tokens of the tile in the slice and allowed by the mask
-  template <class F> __device__ __forceinline__ void operator()(F&& f) const {
-#pragma unroll
-    for (int i = 0; i < G; ++i) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        f(i, j, ((allow >> (4 * i + j)) & 1ull) ? v[i][j] : neg_inf<W>(), 4 * (gb + BLOCK * i) + j);
-    }
-  }
-};
-
+// are masked or outside the slice have the value -inf. The tile itself dies
+// after the statistics pass: MemVisit reads every token again from memory,
+// CandVisit only the groups that can hold a candidate.
 template <int DT, bool VEC, int G> struct MemVisit {
   using W = typename Ty<DT>::W;
   RowView<DT, VEC> view;
@@ -1648,6 +1638,54 @@ template <int DT, bool VEC, int G> struct MemVisit {
     }
   }
 };
+
+// The slice's tokens in the groups marked in `cmask` (bit i: group row i of
+// the tile may hold a candidate), read again from memory four groups at a
+// time, in the tile's order; masked tokens have the value -inf. groups(f)
+// calls f(i, x[4]) per marked group with the raw values.
+template <int DT, bool VEC, int G> struct CandVisit {
+  using W = typename Ty<DT>::W;
+  RowView<DT, VEC> view;
+  uint32_t cmask;
+  int gb;
+  uint64_t allow;
+  template <class F> __device__ __forceinline__ void groups(F&& f) const {
+    uint32_t m = cmask;
+    while (__ballot(m != 0)) {
+      int idx[4];
+      bool has[4];
+      W x[4][4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        has[q] = m != 0;
+        idx[q] = has[q] ? __ffs(m) - 1 : 0;
+        m = has[q] ? m & (m - 1) : m;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (has[q]) view.load(gb + BLOCK * idx[q], x[q]);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (has[q]) f(idx[q], x[q]);
+      }
+    }
+  }
+  template <class F> __device__ __forceinline__ void operator()(F&& f) const {
+    groups([&](int i, const W (&x)[4]) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) f(i, j, ((allow >> (4 * i + j)) & 1ull) ? x[j] : neg_inf<W>(), 4 * (gb + BLOCK * i) + j);
+    });
+  }
+};
+
+// The groups of the tile whose maximum reaches `floor`, as a bit mask.
+template <class W, int G> __device__ __forceinline__ uint32_t groups_reaching(const W (&gm)[G], W floor) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < G; ++i) m |= uint32_t(gm[i] >= floor) << i;
+  return m;
+}
 
 // One bit per token where pred(value, id) holds (valid tokens only).
 template <class W, class Visit, class Pred>
@@ -1773,7 +1811,7 @@ __device__ __forceinline__ void slice_cut(const Visit& visit, int L, W floor, Sh
 // ---------------------------------------------------------------------------
 // The kernel.
 template <int DT, bool VEC, int G>
-__global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
+__global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4))) es_main(es_arguments a, Plan pl) {
   using W = typename Ty<DT>::W;
   __shared__ Shared<W> sh;
   const int tid = threadIdx.x;
@@ -1822,12 +1860,15 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
   const int n_in = g1 > gb ? min(G, (g1 - gb + BLOCK - 1) / BLOCK) : 0;  // groups of the tile in the slice
   uint64_t allow = 4 * n_in >= 64 ? ~0ull : (1ull << (4 * n_in)) - 1ull;
   if (a.mask) {
+    // Group gb + BLOCK * i has its bits in mask word (gb >> 3) + 32 i, at the
+    // same shift for every i.
     uint64_t mbits = 0;
-    const int32_t* mrow = a.mask + row * a.mask_s0;
+    const int32_t* mp = a.mask + row * a.mask_s0 + int64_t(gb >> 3) * a.mask_s1;
+    const int64_t step = 32 * a.mask_s1;
+    const int shift = (4 * gb) & 31;
 #pragma unroll
     for (int i = 0; i < G; ++i) {
-      const int g = min(gb + BLOCK * i, g1 - 1);
-      mbits |= uint64_t((uint32_t(mrow[int64_t((4 * g) >> 5) * a.mask_s1]) >> ((4 * g) & 31)) & 0xfu) << (4 * i);
+      if (i < n_in) mbits |= uint64_t((uint32_t(mp[i * step]) >> shift) & 0xfu) << (4 * i);
     }
     allow &= mbits;
   }
@@ -1850,44 +1891,41 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
   const int j_thr = (L + WAVES - 1) / WAVES;  // thread maxima per wave behind the candidate threshold
 
   // ---- Statistics (reference: fused.cuh:409-519 row_stats). ----
-  // Fast pass: per-group maxima, the slice's maximum over its own groups (the
-  // candidate threshold counts distinct tokens through it, so the copies past
-  // the slice's end are left out) and a non-finite detector over the tile
-  // (fma(x, 0, acc) turns NaN for a NaN or infinite x and stays so).
-  auto group_max = [&](int i) {
-    const W m01 = v[i][0] > v[i][1] ? v[i][0] : v[i][1], m23 = v[i][2] > v[i][3] ? v[i][2] : v[i][3];
-    return m01 > m23 ? m01 : m23;
-  };
+  // One pass over the tile, which dies here: per-group maxima (all that later
+  // steps keep), the slice's maximum and, when it is needed, its lowest ID
+  // (IDs rise with (i, thread, j)), and a non-finite detector over the tile
+  // (fma(x, 0, acc) turns NaN for a NaN or infinite x and stays so). Groups
+  // past the slice's end are copies: their maxima are -inf.
+  const bool track_first = !sorted_list;  // greedy rows, lists a wave cannot take, the full-row path
+  W gm[G];
   W mx = neg_inf<W>(), nf = W(0);
+  int fid_l = INT_MAX;
 #pragma unroll
   for (int i = 0; i < G; ++i) {
-    const W gmi = group_max(i);
+    const W m01 = v[i][1] > v[i][0] ? v[i][1] : v[i][0], m23 = v[i][3] > v[i][2] ? v[i][3] : v[i][2];
+    const int jm = m23 > m01 ? (v[i][3] > v[i][2] ? 3 : 2) : (v[i][1] > v[i][0] ? 1 : 0);
+    const W gmi = m23 > m01 ? m23 : m01;
 #pragma unroll
     for (int j = 0; j < 4; ++j) nf = fma(v[i][j], W(0), nf);
-    mx = i < n_in && gmi > mx ? gmi : mx;
-  }
-  // The wave's maximum and its lowest ID (IDs rise with (i, thread, j)).
-  auto wave_max_id = [&](W m, uint64_t ok_bits) {
-    struct MI { W v; int id; };
-    const W wmax = wave_all(m, [](W x, W y) { return x > y ? x : y; }, neg_inf<W>());
-    int id = INT_MAX;
-    if (m == wmax && wmax > neg_inf<W>()) {
-#pragma unroll
-      for (int i = G - 1; i >= 0; --i) {
-#pragma unroll
-        for (int j = 3; j >= 0; --j)
-          if (((ok_bits >> (4 * i + j)) & 1ull) && v[i][j] == wmax) id = 4 * (gb + BLOCK * i) + j;
-      }
+    gm[i] = i < n_in ? gmi : neg_inf<W>();
+    if (track_first) {
+      const bool up = gm[i] > mx;
+      fid_l = up ? 4 * (gb + BLOCK * i) + jm : fid_l;
+      mx = up ? gm[i] : mx;
+    } else {
+      mx = gm[i] > mx ? gm[i] : mx;
     }
-    return MI{wmax, wave_all(id, [](int x, int y) { return x < y ? x : y; }, INT_MAX)};
-  };
+  }
   {
-    const auto wm = wave_max_id(mx, 4 * n_in >= 64 ? ~0ull : (1ull << (4 * n_in)) - 1ull);
+    const W wmax = wave_all(mx, [](W x, W y) { return x > y ? x : y; }, neg_inf<W>());
+    const int wid = track_first ? wave_all(mx == wmax && wmax > neg_inf<W>() ? fid_l : INT_MAX,
+                                           [](int x, int y) { return x < y ? x : y; }, INT_MAX)
+                                : INT_MAX;
     const W tw = L > 0 ? key_value(wave_kth_largest(order_key(mx), j_thr)) : neg_inf<W>();
     const int nonfinite_w = __ballot(!(nf == W(0))) != 0;
     if (lane == 0) {
-      sh.st_max[wave_id()] = wm.v;
-      sh.st_id[wave_id()] = wm.id;
+      sh.st_max[wave_id()] = wmax;
+      sh.st_id[wave_id()] = wid;
       sh.st_bad[wave_id()] = nonfinite_w;
       sh.st_thr[wave_id()] = tw;
     }
@@ -1910,23 +1948,38 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
 #pragma unroll
   for (int w = 0; w < WAVES; ++w) special |= sh.st_bad[w];
   if (special || a.mask || !VEC) {
-    // Exact pass: a non-finite value, a mask or element loads. NaN/+inf
-    // anywhere (even masked) makes the row invalid; valid tokens are the
-    // allowed ones above -inf, and the group maxima are taken over them.
-    int bad_l = 0, valid_l = 0, fid_l = INT_MAX;
+    // Exact pass over the slice read again: a non-finite value, a mask or
+    // element loads. NaN/+inf anywhere (even masked) makes the row invalid;
+    // valid tokens are the allowed ones above -inf, and the group maxima are
+    // taken over them.
+    int bad_l = 0, valid_l = 0;
     W m2 = neg_inf<W>();
+    fid_l = INT_MAX;
+    // Four groups in flight at a time (the scheduling barrier keeps the
+    // compiler from hoisting every load, which would hold a second tile).
 #pragma unroll
-    for (int i = 0; i < G; ++i) {
+    for (int i0 = 0; i0 < G; i0 += 4) {
+      W x[4][4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const W x = v[i][j];
-        bad_l |= x != x || x == W(INFINITY);
-        const bool ok = ((allow >> (4 * i + j)) & 1ull) && x > neg_inf<W>();
-        valid_l += ok;
-        const bool up = ok && x > m2;
-        fid_l = up ? 4 * (gb + BLOCK * i) + j : fid_l;
-        m2 = up ? x : m2;
+      for (int q = 0; q < 4 && i0 + q < G; ++q) view.load(min(gb + BLOCK * (i0 + q), g1 - 1), x[q]);
+#pragma unroll
+      for (int q = 0; q < 4 && i0 + q < G; ++q) {
+        const int i = i0 + q;
+        W g2 = neg_inf<W>();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const W y = x[q][j];
+          bad_l |= y != y || y == W(INFINITY);
+          const bool ok = ((allow >> (4 * i + j)) & 1ull) && y > neg_inf<W>();
+          valid_l += ok;
+          const bool up = ok && y > m2;
+          fid_l = up ? 4 * (gb + BLOCK * i) + j : fid_l;
+          m2 = up ? y : m2;
+          g2 = ok && y > g2 ? y : g2;
+        }
+        gm[i] = g2;
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
     struct MI { W v; int id; };
     const MI wm = wave_all(MI{m2, fid_l}, [](MI x, MI y) { return (y.v > x.v || (y.v == x.v && y.id < x.id)) ? y : x; },
@@ -1957,48 +2010,43 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
   if (bad) need = 0;
 
   // ---- Candidates for a list row. ----
-  // The tile serves the first selection; anything after it re-reads memory.
-  const TileVisit<W, G> tile{v, gb, allow};
+  // Only groups whose maximum reaches the threshold are read again (they are
+  // few: the slice's top tokens); the rest of the slice is never revisited.
   const MemVisit<DT, VEC, G> mem(a, row, view, gb, g1, pl.groups);
   double frontier = -INFINITY, psum = 0, perr = 0;
   int n_cand = 0, pruned = 0, fid = INT_MAX;
   if (sorted_list && need > 0) {
     // Top-k rows: every valid token >= the threshold (at least L of them),
-    // stored straight from the tile in any order; the merge wave selects.
-    // Complete down to (thr, every ID), or entirely when thr is -inf. Only
-    // groups whose maximum reaches the threshold are looked into.
+    // stored in any order; the merge wave selects. Complete down to (thr,
+    // every ID), or entirely when thr is -inf.
     const W thr = need < valid ? thr_all : neg_inf<W>();
     const W take_from = thr > W(-3.4028234663852886e38) ? thr : W(-3.4028234663852886e38);
+    const CandVisit<DT, VEC, G> cand{view, groups_reaching<W, G>(gm, take_from), gb, allow};
     Cand<W>* out = candidates<W>(a, row) + slice * pl.cap_slice;
-    // A group may hold a candidate when it is in the slice and its maximum
-    // reaches the threshold (masked tokens are excluded token by token). Its
-    // candidates take slots from an LDS counter and are stored at once; slots
-    // past the list's capacity are not written (the exact cut below then
-    // rewrites the list).
+    // Each candidate group takes slots from an LDS counter and stores its
+    // tokens at once; slots past the capacity are not written (the exact cut
+    // below then rewrites the list).
     const int limit = pl.cap_slice;
+    cand.groups([&](int i, const W (&x)[4]) {
+      int cnt = 0;
 #pragma unroll
-    for (int i = 0; i < G; ++i) {
-      if (i < n_in && group_max(i) >= take_from) {
-        int cnt = 0;
+      for (int j = 0; j < 4; ++j) cnt += ((allow >> (4 * i + j)) & 1ull) && x[j] >= take_from;
+      if (cnt) {
+        int o = atomicAdd(&sh.appended, cnt);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) cnt += ((allow >> (4 * i + j)) & 1ull) && v[i][j] >= take_from;
-        if (cnt) {
-          int o = atomicAdd(&sh.appended, cnt);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            if (((allow >> (4 * i + j)) & 1ull) && v[i][j] >= take_from) {
-              if (o < limit) {
-                Cand<W> c{};
-                c.v = v[i][j];
-                c.id = 4 * (gb + BLOCK * i) + j;
-                out[o] = c;
-              }
-              ++o;
+        for (int j = 0; j < 4; ++j) {
+          if (((allow >> (4 * i + j)) & 1ull) && x[j] >= take_from) {
+            if (o < limit) {
+              Cand<W> c{};
+              c.v = x[j];
+              c.id = 4 * (gb + BLOCK * i) + j;
+              out[o] = c;
             }
+            ++o;
           }
         }
       }
-    }
+    });
     __syncthreads();
     const int total = sh.appended;
     if (total <= limit) {
@@ -2008,13 +2056,13 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
       // Too many (ties, or a low threshold): exactly the first L instead.
       W cut_v;
       int cut_id;
-      slice_cut<W, G>(mem, L, take_from, sh, &cut_v, &cut_id);
+      slice_cut<W, G>(cand, L, take_from, sh, &cut_v, &cut_id);
       if (tid == 0) sh.appended = 0;
       __syncthreads();
-      const uint64_t cb = collect_bits<W>(mem, [&](W x, int t) { return x > cut_v || (x == cut_v && t <= cut_id); });
+      const uint64_t cb = collect_bits<W>(cand, [&](W x, int t) { return x > cut_v || (x == cut_v && t <= cut_id); });
       const int cm = __popcll(cb);
       const int cs = cm ? atomicAdd(&sh.appended, cm) : 0;
-      if (cm) publish_taken<W>(mem, cb, out + cs);
+      if (cm) publish_taken<W>(cand, cb, out + cs);
       n_cand = L;
       frontier = double(cut_v);
       fid = cut_id;
@@ -2025,7 +2073,8 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
     // Tokens at or above the threshold: one bit per token of this thread.
     // -inf is never taken: the threshold is raised to the lowest finite value.
     const W take_from = thr > W(-3.4028234663852886e38) ? thr : W(-3.4028234663852886e38);
-    uint64_t take_bits = collect_bits<W>(tile, [&](W x, int) { return x >= take_from; });
+    const CandVisit<DT, VEC, G> cand{view, groups_reaching<W, G>(gm, take_from), gb, allow};
+    uint64_t take_bits = collect_bits<W>(cand, [&](W x, int) { return x >= take_from; });
     int mine = __popcll(take_bits);
     int total;
     int offset = block_scan_add(mine, sh.ired, &total) - mine;
@@ -2036,8 +2085,8 @@ __global__ void __launch_bounds__(BLOCK) es_main(es_arguments a, Plan pl) {
       const int L = min(need, cap);
       W cut_v;
       int cut_id;
-      slice_cut<W, G>(mem, L, take_from, sh, &cut_v, &cut_id);
-      take_bits = collect_bits<W>(mem, [&](W x, int t) { return x > cut_v || (x == cut_v && t <= cut_id); });
+      slice_cut<W, G>(cand, L, take_from, sh, &cut_v, &cut_id);
+      take_bits = collect_bits<W>(cand, [&](W x, int t) { return x > cut_v || (x == cut_v && t <= cut_id); });
       mine = __popcll(take_bits);
       offset = block_scan_add(mine, sh.ired, &total) - mine;
       thr = cut_v;

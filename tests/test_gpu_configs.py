@@ -80,3 +80,19 @@ def test_greedy_and_plain_temperature_rows():
     rng = RngKey([int(s) for s in keys["seed"]], [int(s) for s in keys["stream"]], keys["positions"])
     expected = expected_for(args, work["offsets"], work["ids"], params=RequestParams(**work["params"]), rng=rng)
     np.testing.assert_array_equal(out.tokens.cpu().numpy()[:128], expected.tokens)
+
+
+def test_top_k_row_that_falls_back_to_the_full_row():
+    """A flat row with k = 64 over 38 slices: the candidate union (38 x 64
+    tokens) exceeds what the wave and the block list take, so the row is
+    finished on the full-row path, which needs the row's greedy token (found
+    by the merge wave, since slices of top-k rows do not track it)."""
+    import torch
+    from tests.gpu_helpers import run_and_compare
+
+    rows = np.zeros((2, 151936), np.float32)
+    rows[1, 7777] = 0.5  # a single maximum away from token 0
+    out, _, args = run_and_compare(rows, [0, 1, 2], np.empty((2, 0), np.int64), dtype=torch.float32,
+                                   params=RequestParams(top_k=64, temperature=0.8))
+    routes = row_diagnostics(args["plan"], 2)
+    assert all(route >= 100 for route, _ in routes), routes
