@@ -10,13 +10,20 @@ settings. Rows come from the peaked generator: base N(mu, sigma^2) with
 mu ~ U(-5, 0), sigma ~ U(2, 4); one token + U(6, 14); 15 tokens + U(0, 8);
 every even row rounded to the bf16 grid (values stay fp32).
 
-Reported per cell: median and mean event time per call (warm: logits resident
-as right after the LM head), median time after a 2 GiB read that evicts the
-256 MB Infinity Cache (cold), and the HBM roofline of the call: algorithmic
-bytes = one read of every logit row (+ outputs and parameters, < 0.1%).
-``cpu_baseline`` times the FP64 oracle (oracle/, the reference algorithm with
-its per-token scalar Philox) on a bounded sample of the headline rows, single
-threaded.
+Reported per cell, with every timed call queued behind a spin kernel so that
+calls run back to back and events hold GPU time only: the median and mean time
+per call through the C ABI (the value), the same through the torch op (which
+also records the plan's completion event), the slice-stream kernel (es_main)
+and the per-row finishing kernel (es_finish) timed apart by an event the
+library records between them, and cold medians after a 2 GiB read that evicts
+the 256 MB Infinity Cache. The roofline is es_main's: algorithmic bytes (one
+read of every logit row, plus parameters and outputs, < 0.1%) over its average
+warm duration; ``traffic`` is its HBM bytes per launch from the committed
+FETCH_SIZE / WRITE_SIZE counter summary. A plain copy kernel of the headline
+logits' size is timed first (the stream-copy rate measured on the device, and
+the counters' calibration). ``cpu_baseline`` times the FP64 oracle (oracle/,
+the reference algorithm with its per-token scalar Philox) on a bounded sample
+of the headline rows, single threaded.
 """
 import argparse
 import json
@@ -121,63 +128,220 @@ def algorithmic_bytes(work):
     return rows * vocab * 4 + params + outputs
 
 
-def time_cell(name, steps, warmup):
+class Events:
+    """HIP timing events created with hipEventDisableSystemFence.
+
+    An event that ends in a system-scope fence (torch.cuda.Event's) costs
+    about 3.7 us of GPU time between back-to-back calls; without the fence the
+    marker costs little and times the work it brackets more closely (the
+    flag's documented use). Driven through the HIP runtime that torch loaded.
+    """
+    DISABLE_SYSTEM_FENCE = 0x20000000
+
+    def __init__(self):
+        import ctypes
+        self._ct = ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.made = []
+
+    def create(self, n):
+        out = []
+        for _ in range(n):
+            e = self._ct.c_void_p()
+            if self.hip.hipEventCreateWithFlags(self._ct.byref(e), self._ct.c_uint(self.DISABLE_SYSTEM_FENCE)):
+                raise RuntimeError("hipEventCreateWithFlags failed")
+            out.append(e.value)
+        self.made += out
+        return out
+
+    def record(self, event, stream):
+        if self.hip.hipEventRecord(event, stream.cuda_stream):
+            raise RuntimeError("hipEventRecord failed")
+
+    def us(self, a, b):
+        ms = self._ct.c_float()
+        self.hip.hipEventSynchronize(b)
+        if self.hip.hipEventElapsedTime(self._ct.byref(ms), a, b):
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value * 1000.0
+
+    def destroy(self):
+        for e in self.made:
+            self.hip.hipEventDestroy(e)
+        self.made = []
+
+
+_SPIN_RATE = []
+
+
+def queue_ahead(us):
+    """Enqueues a spin kernel of about `us` microseconds on the current stream.
+
+    The calls enqueued behind it then run back to back, so the events around
+    each call hold GPU time only, never the host's launch time. Callers ask
+    for about 120 us per queued call."""
     import torch
+    if not _SPIN_RATE:
+        torch.cuda._sleep(1000)  # the first launch also loads the kernel: keep it out of the calibration
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        torch.cuda._sleep(4_000_000)
+        b.record()
+        b.synchronize()
+        _SPIN_RATE.append(4_000_000 / (a.elapsed_time(b) * 1000.0))  # spin cycles per microsecond
+    torch.cuda._sleep(int(_SPIN_RATE[0] * us))
+
+
+def time_cell(name, steps, warmup):
+    """Per-call GPU time of one cell, the two kernels timed apart, and cold calls.
+
+    Every timed call is queued behind a spin kernel, so calls run back to back.
+    - value: the C ABI (es_launch) with an event before and after each call;
+    - op: the same through exactsample_amd.cuda.verify (the torch op; it also
+      records the plan's completion event each call, which costs GPU time);
+    - split: es_launch with a third event recorded by the library between the
+      slice-stream kernel (es_main) and the per-row finishing kernel
+      (es_finish), via es_set_split_event: the dominant kernel's duration for
+      the roofline;
+    - cold: split calls, each after a 2 GiB read that evicts the 256 MB
+      Infinity Cache.
+    """
+    import torch
+    from exactsample_amd import capi
     from exactsample_amd.cuda import verify
 
     work = CELLS[name]()
     args = device_args(work)
     stream = torch.cuda.current_stream()
+    lib = capi.load()
+    p, r, o = args["params"], args["rng"], args["out"]
+    abi = capi.from_tensors(args["target_logits"], args["cu_rows"], args["draft_ids"], None, p.temperature,
+                            p.top_k, p.top_p, p.min_p, p.draft_kind, r.seed, r.stream_id, r.positions, None,
+                            args["plan"].workspace, o.tokens, o.accepted_len, o.status, o.path_used,
+                            mode=0 if work["mode"] == "ratio" else 1, max_draft=args["plan"].max_draft)
+    requests = len(work["offsets"]) - 1
+    ev = Events()
 
-    def call():
-        return verify(**args, mode=work["mode"], top_k_top_p=True)
+    def op():
+        verify(**args, mode=work["mode"], top_k_top_p=True)
+
+    def launch():
+        capi.launch(lib, abi, stream)
 
     for _ in range(warmup):
-        call()
+        op()
+    op_tokens = o.tokens[:requests].clone()
+    for _ in range(warmup):
+        launch()
     torch.cuda.synchronize()
-    # Per-call events on the stream the kernels run on.
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    stops = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    t0 = time.perf_counter()
-    for i in range(steps):
-        starts[i].record(stream)
-        call()
-        stops[i].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per_call = np.array([s.elapsed_time(e) * 1000.0 for s, e in zip(starts, stops)])
-    # Cold: evict L2 and the Infinity Cache with a 2 GiB read first.
+    if not torch.equal(op_tokens, o.tokens[:requests]):
+        raise RuntimeError("the C ABI and the torch op disagree")
+
+    def per_call(fn, n, mid=False, before=None):
+        a, b = ev.create(n), ev.create(n)
+        m = ev.create(n) if mid else None
+        if before is None:
+            queue_ahead(n * 120.0)
+        t0 = time.perf_counter()
+        try:
+            for i in range(n):
+                if before is not None:
+                    before()
+                if mid:
+                    lib.es_set_split_event(m[i])
+                ev.record(a[i], stream)
+                fn()
+                ev.record(b[i], stream)
+                if before is not None:
+                    ev.us(a[i], b[i])  # one cold call at a time
+        finally:
+            lib.es_set_split_event(None)
+        host = (time.perf_counter() - t0) / n * 1e6
+        torch.cuda.synchronize()
+        if not mid:
+            return np.array([ev.us(x, y) for x, y in zip(a, b)]), host
+        return (np.array([ev.us(x, y) for x, y in zip(a, m)]), np.array([ev.us(x, y) for x, y in zip(m, b)]),
+                host)
+
+    calls, host_abi = per_call(launch, steps)
+    op_calls, host_op = per_call(op, steps)
+    main, finish, _ = per_call(launch, steps, mid=True)
     flush = torch.ones(512 << 20, dtype=torch.float32, device="cuda")
-    cold = []
-    for _ in range(min(steps, 30)):
-        flush.sum()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record(stream)
-        call()
-        e.record(stream)
-        e.synchronize()
-        cold.append(s.elapsed_time(e) * 1000.0)
+    cold_main, cold_finish, _ = per_call(launch, min(steps, 30), mid=True, before=flush.sum)
+    cold = cold_main + cold_finish
     del flush
+    ev.destroy()
     fallbacks = args["plan"].fallbacks()
     nbytes = algorithmic_bytes(work)
-    med = float(np.median(per_call))
-    return dict(rows=int(work["rows"].shape[0]), requests=int(len(work["offsets"]) - 1),
-                median_us=med, mean_us=float(per_call.mean()), p10_us=float(np.percentile(per_call, 10)),
-                p90_us=float(np.percentile(per_call, 90)), cold_median_us=float(np.median(cold)),
-                wall_ms=wall * 1000.0, bytes=int(nbytes), achieved_gbs=nbytes / (med * 1e-6) / 1e9,
-                frac=nbytes / (med * 1e-6) / HBM_PEAK, fallbacks=int(fallbacks),
-                accepted_mean=float(args["out"].accepted_len[:len(work["offsets"]) - 1].float().mean().item()))
+    med = float(np.median(calls))
+    main_avg = float(main.mean())
+    return dict(rows=int(work["rows"].shape[0]), requests=requests,
+                median_us=med, mean_us=float(calls.mean()), p10_us=float(np.percentile(calls, 10)),
+                p90_us=float(np.percentile(calls, 90)),
+                op_median_us=float(np.median(op_calls)), op_mean_us=float(op_calls.mean()),
+                host_us_per_call_abi=host_abi, host_us_per_call_op=host_op,
+                es_main_avg_us=main_avg, es_main_median_us=float(np.median(main)),
+                es_finish_avg_us=float(finish.mean()), es_finish_median_us=float(np.median(finish)),
+                cold_median_us=float(np.median(cold)), cold_es_main_median_us=float(np.median(cold_main)),
+                bytes=int(nbytes), call_gbs=nbytes / (med * 1e-6) / 1e9,
+                es_main_gbs=nbytes / (main_avg * 1e-6) / 1e9,
+                cold_es_main_gbs=nbytes / (float(np.median(cold_main)) * 1e-6) / 1e9,
+                fallbacks=int(fallbacks),
+                accepted_mean=float(o.accepted_len[:requests].float().mean().item()))
+
+
+def copy_rate(nbytes, launches=10):
+    """A plain copy kernel (torch.neg) over a buffer of `nbytes`: event GB/s of
+    read + write, and the calibration launches for the FETCH_SIZE / WRITE_SIZE
+    counters (each launch reads and writes exactly `nbytes`)."""
+    import torch
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    ev = Events()
+    a, b = ev.create(launches), ev.create(launches)
+    stream = torch.cuda.current_stream()
+    queue_ahead(launches * 120.0)
+    for i in range(launches):
+        ev.record(a[i], stream)
+        torch.neg(src, out=dst)
+        ev.record(b[i], stream)
+    torch.cuda.synchronize()
+    us = float(np.median([ev.us(x, y) for x, y in zip(a, b)]))
+    ev.destroy()
+    return dict(bytes_each_way=int(nbytes), median_us=us, gbs=2 * nbytes / (us * 1e-6) / 1e9)
+
+
+def measured_traffic(path=os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                                       "es_main_128x1_traffic.md")):
+    """HBM bytes per es_main launch from the committed FETCH_SIZE / WRITE_SIZE
+    summary (line "traffic_bytes_per_launch: N"), or None."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        return None
+    return None
 
 
 def cpu_baseline(budget_s=12.0):
-    """The FP64 oracle, single-threaded, on headline rows until the budget is spent."""
+    """The FP64 oracle, single-threaded, over the headline rows (cycling through
+    them) until the budget is spent; scaled to one 128-request call."""
     from oracle import RequestParams, RngKey, verify_reference
 
     work = config2()
     rows = work["rows"].astype(np.float64)
     done, t0 = 0, time.perf_counter()
-    while done < len(rows) and time.perf_counter() - t0 < budget_s:
-        r = done
+    while time.perf_counter() - t0 < budget_s:
+        r = done % len(rows)
         verify_reference(rows[r:r + 1], [0, 1], np.empty((1, 0), np.int64), params=RequestParams(**QWEN),
                          rng=RngKey(int(work["keys"]["seed"][r]), int(work["keys"]["stream"][r]),
                                     [int(work["keys"]["positions"][r])]),
@@ -185,10 +349,11 @@ def cpu_baseline(budget_s=12.0):
         done += 1
     elapsed = time.perf_counter() - t0
     per_row = elapsed / done
-    return dict(value=per_row * 128 * 1e6, unit="us/call (128 requests, extrapolated from the sample)",
+    return dict(value=per_row * 128 * 1e6, unit="us/call (128 requests, from the sample's time per row)",
                 cores=1, kind="port",
-                sample=f"{done} of the 128 headline rows ({elapsed:.1f} s) through oracle.verify_reference "
-                       f"with per-token scalar Philox; the FP64 restatement of reference.py")
+                sample=f"{done} rows of the 128-row headline batch, cycled ({elapsed:.1f} s), through "
+                       f"oracle.verify_reference with per-token scalar Philox: the FP64 restatement of "
+                       f"reference.py, single threaded")
 
 
 def main():
@@ -209,6 +374,8 @@ def main():
         return 2
     from exactsample_amd.cuda import load_library
     load_library()
+    copy = copy_rate(VOCAB * 4 * 128)
+    print(json.dumps({"copy": copy}), file=sys.stderr, flush=True)
     cells = {}
     for name in args.cells.split(","):
         cells[name] = time_cell(name, args.steps, args.warmup)
@@ -230,10 +397,14 @@ def main():
         "data": "synthetic",
         "config": {"workload": "128 requests x 1 row, V=151936 fp32, T=0.6 top-k 20 top-p 0.95 (half the rows on "
                                "the bf16 grid); second cell 64 requests x (4 one-hot drafts + bonus), ratio mode",
-                   "vocab": VOCAB, "cells": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv)
-                                                 for kk, vv in v.items()} for k, v in cells.items()}},
-        "roofline": {"bound": "hbm", "achieved": round(head["achieved_gbs"], 1), "peak": HBM_PEAK / 1e9,
-                     "unit": "GB/s", "frac": round(head["frac"], 4), "traffic": None},
+                   "vocab": VOCAB, "copy_kernel": {k: round(v, 3) if isinstance(v, float) else v
+                                                  for k, v in copy.items()},
+                   "cells": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv)
+                                 for kk, vv in v.items()} for k, v in cells.items()}},
+        "roofline": {"bound": "hbm", "kernel": "es_main (slice stream), 128x1 cell, warm, timed region",
+                     "achieved": round(head["es_main_gbs"], 1), "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": round(head["es_main_gbs"] * 1e9 / HBM_PEAK, 4),
+                     "traffic": measured_traffic()},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

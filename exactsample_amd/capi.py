@@ -48,7 +48,8 @@ class Arguments(ctypes.Structure):
     ]
 
 
-EXPORTS = ["es_workspace_size", "es_launch", "es_error_string", "es_last_hip_error", "es_fallback_counter_offset"]
+EXPORTS = ["es_workspace_size", "es_launch", "es_error_string", "es_last_hip_error", "es_set_split_event",
+           "es_fallback_counter_offset"]
 
 
 def load(path=None):
@@ -62,6 +63,8 @@ def load(path=None):
     lib.es_error_string.argtypes = [ctypes.c_int32]
     lib.es_last_hip_error.restype = ctypes.c_char_p
     lib.es_last_hip_error.argtypes = []
+    lib.es_set_split_event.restype = None
+    lib.es_set_split_event.argtypes = [ctypes.c_void_p]
     lib.es_fallback_counter_offset.restype = ctypes.c_size_t
     lib.es_fallback_counter_offset.argtypes = []
     return lib

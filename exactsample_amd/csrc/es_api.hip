@@ -8,6 +8,7 @@
 namespace {
 constexpr int kBlock = 256;  // threads per block of the kernel
 thread_local char g_last_hip_error[256] = "";
+thread_local hipEvent_t g_split_event = nullptr;
 
 constexpr int64_t elem_size(int dt) { return dt == ES_F64 ? 8 : dt == ES_F32 ? 4 : 2; }
 
@@ -70,6 +71,8 @@ const char* es_error_string(int32_t code) {
 
 const char* es_last_hip_error(void) { return g_last_hip_error; }
 
+void es_set_split_event(void* event) { g_split_event = static_cast<hipEvent_t>(event); }
+
 int32_t es_launch(const es_arguments* args, void* stream_ptr) {
   if (!args) return ES_ERR_NULL_ARGUMENT;
   const es_arguments& a = *args;
@@ -113,10 +116,10 @@ int32_t es_launch(const es_arguments* args, void* stream_ptr) {
   hipError_t err = hipSuccess;
   if (geo.slices > es::MAX_SLICES) return ES_ERR_BAD_DIMENSION;  // vocabularies above ~1M are not supported yet
   switch (a.target.dtype) {
-    case ES_F32: err = es::launch_dtype<ES_F32>(a, pl, geo.g, vectorizable<ES_F32>(a), stream); break;
-    case ES_F64: err = es::launch_dtype<ES_F64>(a, pl, geo.g, vectorizable<ES_F64>(a), stream); break;
-    case ES_F16: err = es::launch_dtype<ES_F16>(a, pl, geo.g, vectorizable<ES_F16>(a), stream); break;
-    default: err = es::launch_dtype<ES_BF16>(a, pl, geo.g, vectorizable<ES_BF16>(a), stream); break;
+    case ES_F32: err = es::launch_dtype<ES_F32>(a, pl, geo.g, vectorizable<ES_F32>(a), stream, g_split_event); break;
+    case ES_F64: err = es::launch_dtype<ES_F64>(a, pl, geo.g, vectorizable<ES_F64>(a), stream, g_split_event); break;
+    case ES_F16: err = es::launch_dtype<ES_F16>(a, pl, geo.g, vectorizable<ES_F16>(a), stream, g_split_event); break;
+    default: err = es::launch_dtype<ES_BF16>(a, pl, geo.g, vectorizable<ES_BF16>(a), stream, g_split_event); break;
   }
   if (err != hipSuccess) {
     snprintf(g_last_hip_error, sizeof(g_last_hip_error), "%s", hipGetErrorString(err));

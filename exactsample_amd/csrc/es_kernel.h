@@ -2317,10 +2317,11 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments a, Plan pl) {
 // Per-dtype launchers, instantiated in one translation unit per dtype.
 namespace es {
 template <int DT, bool VEC, int G>
-hipError_t launch_main(const es_arguments& a, const Plan& pl, hipStream_t stream) {
+hipError_t launch_main(const es_arguments& a, const Plan& pl, hipStream_t stream, hipEvent_t split) {
   const unsigned blocks = unsigned(pl.req_blocks + a.rows * pl.slices);
   hipLaunchKernelGGL((es_main<DT, VEC, G>), dim3(blocks), dim3(BLOCK), 0, stream, a, pl);
   hipError_t err = hipGetLastError();
+  if (err == hipSuccess && split) err = hipEventRecord(split, stream);
   if (err != hipSuccess || a.rows == 0) return err;
   hipLaunchKernelGGL((es_finish<DT, VEC>), dim3(unsigned(a.rows)), dim3(BLOCK), 0, stream, a, pl);
   return hipGetLastError();
@@ -2335,12 +2336,13 @@ template <> struct Tiles<ES_F64> { static constexpr int n = 1; static constexpr 
 
 // Contiguous rows aligned to a group of four use vector loads; any other
 // layout uses element loads with the smallest tile.
-template <int DT> hipError_t launch_dtype(const es_arguments& a, const Plan& pl, int g, bool vec, hipStream_t stream) {
-  if (!vec) return launch_main<DT, false, 4>(a, pl, stream);
+template <int DT>
+hipError_t launch_dtype(const es_arguments& a, const Plan& pl, int g, bool vec, hipStream_t stream, hipEvent_t split) {
+  if (!vec) return launch_main<DT, false, 4>(a, pl, stream, split);
   if constexpr (Tiles<DT>::n == 3) {
-    if (g == 16) return launch_main<DT, true, 16>(a, pl, stream);
-    if (g == 8) return launch_main<DT, true, 8>(a, pl, stream);
+    if (g == 16) return launch_main<DT, true, 16>(a, pl, stream, split);
+    if (g == 8) return launch_main<DT, true, 8>(a, pl, stream, split);
   }
-  return launch_main<DT, true, 4>(a, pl, stream);
+  return launch_main<DT, true, 4>(a, pl, stream, split);
 }
 }  // namespace es

@@ -16,12 +16,14 @@ struct Plan {
   int32_t pad;
 };
 
-// Launches the kernel for logits of dtype DT with a register tile of g groups
-// of four per thread; vec selects vector loads (contiguous, aligned rows).
-template <int DT> hipError_t launch_dtype(const es_arguments& a, const Plan& pl, int g, bool vec, hipStream_t stream);
-extern template hipError_t launch_dtype<ES_F32>(const es_arguments&, const Plan&, int, bool, hipStream_t);
-extern template hipError_t launch_dtype<ES_BF16>(const es_arguments&, const Plan&, int, bool, hipStream_t);
-extern template hipError_t launch_dtype<ES_F16>(const es_arguments&, const Plan&, int, bool, hipStream_t);
-extern template hipError_t launch_dtype<ES_F64>(const es_arguments&, const Plan&, int, bool, hipStream_t);
+// Launches the two kernels of a call for logits of dtype DT with a register
+// tile of g groups of four per thread; vec selects vector loads (contiguous,
+// aligned rows). A non-null split event is recorded between the kernels.
+template <int DT> hipError_t launch_dtype(const es_arguments& a, const Plan& pl, int g, bool vec, hipStream_t stream,
+                                          hipEvent_t split);
+extern template hipError_t launch_dtype<ES_F32>(const es_arguments&, const Plan&, int, bool, hipStream_t, hipEvent_t);
+extern template hipError_t launch_dtype<ES_BF16>(const es_arguments&, const Plan&, int, bool, hipStream_t, hipEvent_t);
+extern template hipError_t launch_dtype<ES_F16>(const es_arguments&, const Plan&, int, bool, hipStream_t, hipEvent_t);
+extern template hipError_t launch_dtype<ES_F64>(const es_arguments&, const Plan&, int, bool, hipStream_t, hipEvent_t);
 
 }  // namespace es

@@ -94,6 +94,13 @@ const char* es_error_string(int32_t code);
 /* The last HIP runtime error string seen by es_launch on this thread ("" if none). */
 const char* es_last_hip_error(void);
 
+/* Timing hook with no counterpart in the reference, for benchmarks and profilers
+ * that want the two kernels of a call timed apart. When `event` (a hipEvent_t) is
+ * non-null, every later es_launch on this thread records it on the call's stream
+ * between the slice-stream kernel and the per-row finishing kernel; NULL turns it
+ * off. Recording adds a stream marker, so leave it off outside measurement. */
+void es_set_split_event(void* event);
+
 /* Offset of the FP64 recomputation counter in the workspace (a uint32 written by
  * each call; read it after the call completes). Replaces workspace word 1 read at
  * python/exactsample/cuda.py:109-114. */
