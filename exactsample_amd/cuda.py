@@ -83,12 +83,31 @@ def load_library(path: str | os.PathLike[str] | None = None) -> None:
     torch.ops.load_library(str(library.resolve()))
 
 
+_PLAN_DIMENSIONS = ("max_rows", "max_requests", "max_draft", "vocab")
+
+
+def _plan_dimension(name: str, value: Any) -> int:
+    """A plan size: a plain int, at least 1 for the vocabulary and 0 otherwise, below 2**31."""
+    smallest = 1 if name == "vocab" else 0
+    is_integer = isinstance(value, int) and not isinstance(value, bool)
+    if not is_integer or value < smallest:
+        raise ValueError(f"{name} must be a nonnegative integer (vocab must be positive)")
+    if value >= 2**31:
+        raise ValueError(f"{name} exceeds kernel int32 indexing")
+    return value
+
+
 class CudaPlan:
     """A workspace for one call at a time. Calls on one stream queue safely;
     a call on another stream while one is in flight is refused.
 
     Inputs and outputs must stay unchanged until ``synchronize`` or stream
     order establishes completion. Graph capture is not supported.
+
+    State: ``workspace`` (zeroed once: the kernels' arrival counters start at
+    zero and every call leaves them at zero), a non-blocking lock that admits
+    one host call at a time, the stream of the last call and an event recorded
+    after it (which answers "is the last call still running?").
     """
 
     def __init__(self, max_rows: int, max_requests: int, max_draft: int, vocab: int,
@@ -97,61 +116,79 @@ class CudaPlan:
 
         if caps:
             raise ValueError("caps is reserved; v1 supports the default capabilities only")
-        for name, value in (("max_rows", max_rows), ("max_requests", max_requests),
-                            ("max_draft", max_draft), ("vocab", vocab)):
-            lowest = 1 if name == "vocab" else 0
-            if isinstance(value, bool) or not isinstance(value, int) or value < lowest:
-                raise ValueError(f"{name} must be a nonnegative integer (vocab must be positive)")
-            if value >= 2**31:
-                raise ValueError(f"{name} exceeds kernel int32 indexing")
-        device = torch.device(device)
-        if device.type != "cuda":
+        sizes = dict(zip(_PLAN_DIMENSIONS, (max_rows, max_requests, max_draft, vocab)))
+        for name, value in sizes.items():
+            _plan_dimension(name, value)
+        where = torch.device(device)
+        if where.type != "cuda":
             raise ValueError("CudaPlan requires a CUDA device")
-        self.device = torch.device("cuda", torch.cuda.current_device() if device.index is None else device.index)
-        self.max_rows, self.max_requests, self.max_draft, self.vocab = max_rows, max_requests, max_draft, vocab
+        index = torch.cuda.current_device() if where.index is None else where.index
+        self.device = torch.device("cuda", index)
+        self.max_rows, self.max_requests, self.max_draft, self.vocab = (sizes[k] for k in _PLAN_DIMENSIONS)
         # Kept sets of at most this many tokens are finished as an FP64 list;
         # 0 sends every filtered row to the full-row path (tests use both).
         self.list_max = 256
         self.reference = reference
-        self.workspace_bytes = int(c_library().es_workspace_size(max_rows, vocab, 1 if reference else 0))
+        lib = c_library()
+        self.workspace_bytes = int(lib.es_workspace_size(max_rows, vocab, int(bool(reference))))
         if self.workspace_bytes == 0:
             raise ValueError("workspace size overflow")
-        # Zeroed once: the kernels' arrival counters start at zero and every
-        # call leaves them at zero.
         self.workspace = torch.zeros(self.workspace_bytes, dtype=torch.uint8, device=self.device)
-        self._fallback_offset = int(c_library().es_fallback_counter_offset())
+        self._fallback_offset = int(lib.es_fallback_counter_offset())
         self._lock = threading.Lock()
-        self._event = torch.cuda.Event(enable_timing=False)
+        self._done = torch.cuda.Event(enable_timing=False)
         self._last_stream = None
-        self._references = ()
-        self._event.record(torch.cuda.current_stream(self.device))  # create the event outside the hot path
-        self._event.synchronize()
+        self._held = ()
+        # The event's first record creates it: do that here, not on the first call.
+        self._done.record(torch.cuda.current_stream(self.device))
+        self._done.synchronize()
 
     def allocate_output(self) -> CudaOutput:
         import torch
 
-        rows = self.max_requests
-        return CudaOutput(
-            torch.empty((rows, self.max_draft + 1), device=self.device, dtype=torch.int64),
-            torch.empty(rows, device=self.device, dtype=torch.int32),
-            torch.empty(rows, device=self.device, dtype=torch.int32),
-            torch.empty(rows, device=self.device, dtype=torch.int32),
-        )
+        def per_request(*shape, dtype):
+            return torch.empty(shape, device=self.device, dtype=dtype)
+
+        n = self.max_requests
+        return CudaOutput(per_request(n, self.max_draft + 1, dtype=torch.int64), per_request(n, dtype=torch.int32),
+                          per_request(n, dtype=torch.int32), per_request(n, dtype=torch.int32))
 
     def fallbacks(self) -> int:
         """FP64 recomputations the last call needed (synchronizes)."""
         import torch
 
         self.synchronize()
-        start = self._fallback_offset
-        return int(self.workspace[start:start + 4].view(torch.int32).item())
+        word = self.workspace.narrow(0, self._fallback_offset, 4)
+        return int(word.view(torch.int32).item())
 
     def synchronize(self) -> None:
         """Waits for this plan's last call; the workspace may then be used on any stream."""
         with self._lock:
-            self._event.synchronize()
-            self._references = ()
-            self._last_stream = None
+            self._done.synchronize()
+            self._release()
+
+    # -- used by verify -------------------------------------------------
+    def _claim(self, stream) -> None:
+        """Refuses a call on another stream while the last call may still run."""
+        if self._last_stream in (None, stream.cuda_stream):
+            return
+        if not self._done.query():
+            raise RuntimeError("exactsample workspace is in flight on another stream; "
+                               "synchronize or use a separate plan")
+
+    def _enqueued(self, stream, tensors) -> None:
+        """After a launch (or a failed one: work may be partly enqueued), keeps
+        every tensor alive on `stream` and marks the plan busy there."""
+        for t in tensors:
+            if t is not None and t.device == self.device:
+                t.record_stream(stream)
+        self._held = tensors
+        self._last_stream = stream.cuda_stream
+        self._done.record(stream)
+
+    def _release(self) -> None:
+        self._held = ()
+        self._last_stream = None
 
 
 def plan(max_rows: int, max_requests: int, max_draft: int, vocab: int,
@@ -161,6 +198,25 @@ def plan(max_rows: int, max_requests: int, max_draft: int, vocab: int,
 
 _MODES = {"ratio": 0, "coupled": 1}
 _DISPATCH = {"auto": 0, "reference": 1, "fused": 2}
+
+
+def _check_call(target_logits, cu_rows, params, rng, plan, mode, dispatch) -> int:
+    """Host-side checks that need no device data; returns the request count."""
+    if mode not in _MODES or dispatch not in _DISPATCH:
+        raise ValueError("mode must be ratio/coupled; dispatch must be auto/reference/fused")
+    if dispatch == "reference" and not plan.reference:
+        raise ValueError("dispatch='reference' needs a plan made with reference=True")
+    if not (isinstance(params, CudaRequestParams) and isinstance(rng, CudaRngKey)):
+        raise TypeError("CUDA verify requires CudaRequestParams and CudaRngKey containing device tensors")
+    if target_logits.ndim != 2 or cu_rows.ndim != 1 or cu_rows.numel() < 1:
+        raise ValueError("target_logits must be 2D and cu_rows a nonempty 1D tensor")
+    requests = cu_rows.numel() - 1
+    rows, vocab = target_logits.shape
+    if rows > plan.max_rows or requests > plan.max_requests or vocab != plan.vocab:
+        raise ValueError("input exceeds plan capacity or has a different vocabulary")
+    if target_logits.device != plan.device:
+        raise ValueError("input and plan must be on the same CUDA device")
+    return requests
 
 
 def verify(target_logits, cu_rows, draft_ids, *, params: CudaRequestParams,
@@ -181,20 +237,11 @@ def verify(target_logits, cu_rows, draft_ids, *, params: CudaRequestParams,
     """
     import torch
 
-    if mode not in _MODES or dispatch not in _DISPATCH:
-        raise ValueError("mode must be ratio/coupled; dispatch must be auto/reference/fused")
-    if dispatch == "reference" and not plan.reference:
-        raise ValueError("dispatch='reference' needs a plan made with reference=True")
-    if not isinstance(params, CudaRequestParams) or not isinstance(rng, CudaRngKey):
-        raise TypeError("CUDA verify requires CudaRequestParams and CudaRngKey containing device tensors")
-    if target_logits.ndim != 2 or cu_rows.ndim != 1 or cu_rows.numel() < 1:
-        raise ValueError("target_logits must be 2D and cu_rows a nonempty 1D tensor")
-    requests = cu_rows.numel() - 1
-    if target_logits.shape[0] > plan.max_rows or requests > plan.max_requests or target_logits.shape[1] != plan.vocab:
-        raise ValueError("input exceeds plan capacity or has a different vocabulary")
-    if target_logits.device != plan.device:
-        raise ValueError("input and plan must be on the same CUDA device")
+    requests = _check_call(target_logits, cu_rows, params, rng, plan, mode, dispatch)
     load_library()
+    op_args = (target_logits, cu_rows, draft_ids, draft_logits, params.temperature, params.top_k,
+               params.top_p, params.min_p, params.draft_kind, rng.seed, rng.stream_id, rng.positions,
+               mask, plan.workspace, out.tokens, out.accepted_len, out.status, out.path_used)
     with torch.cuda.device(plan.device):
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError("exactsample v1 does not support CUDA graph capture")
@@ -202,29 +249,17 @@ def verify(target_logits, cu_rows, draft_ids, *, params: CudaRequestParams,
         if not plan._lock.acquire(blocking=False):
             raise RuntimeError("exactsample workspace is already in use by another host call")
         try:
-            if (plan._last_stream is not None and plan._last_stream != stream.cuda_stream
-                    and not plan._event.query()):
-                raise RuntimeError("exactsample workspace is in flight on another stream; "
-                                   "synchronize or use a separate plan")
-            tensors = (target_logits, cu_rows, draft_ids, draft_logits, params.temperature, params.top_k,
-                       params.top_p, params.min_p, params.draft_kind, rng.seed, rng.stream_id, rng.positions,
-                       mask, plan.workspace, out.tokens, out.accepted_len, out.status, out.path_used)
-            if any(t is not None and not isinstance(t, torch.Tensor) for t in tensors):
+            plan._claim(stream)
+            present = [t for t in op_args if t is not None]
+            if not all(isinstance(t, torch.Tensor) for t in present):
                 raise TypeError("all CUDA arguments must be preallocated tensors")
-            if any(t is not None and t.requires_grad for t in tensors):
+            if any(t.requires_grad for t in present):
                 raise ValueError("exactsample is an inference operator and does not support autograd")
             try:
-                torch.ops.exactsample.verify_out(*tensors, _MODES[mode], _DISPATCH[dispatch], plan.max_draft,
+                torch.ops.exactsample.verify_out(*op_args, _MODES[mode], _DISPATCH[dispatch], plan.max_draft,
                                                  plan.list_max if top_k_top_p else 0)
             finally:
-                # Work may be partly enqueued even when the launch reports an
-                # error: keep every tensor alive on this stream regardless.
-                for tensor in tensors:
-                    if tensor is not None and tensor.device == plan.device:
-                        tensor.record_stream(stream)
-                plan._references = tensors
-                plan._last_stream = stream.cuda_stream
-                plan._event.record(stream)
+                plan._enqueued(stream, op_args)
             out.num_requests = requests
         finally:
             plan._lock.release()
