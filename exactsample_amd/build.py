@@ -25,7 +25,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "libexactsample_amd.so")
 OPS = os.path.join(HERE, "_exactsample_ops.so")
-KERNEL_UNITS = ["es_f32.hip", "es_bf16.hip", "es_f16.hip", "es_f64.hip", "es_api.hip"]
+KERNEL_UNITS = ["es_f32.hip", "es_bf16.hip", "es_f16.hip", "es_f64.hip", "es_api.hip", "es_selftest.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("EXACTSAMPLE_ARCH", "gfx950")
 

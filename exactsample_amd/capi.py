@@ -49,11 +49,21 @@ class Arguments(ctypes.Structure):
 
 
 EXPORTS = ["es_workspace_size", "es_launch", "es_error_string", "es_last_hip_error", "es_set_split_event",
-           "es_fallback_counter_offset"]
+           "es_check_gumbel", "es_fallback_counter_offset"]
 
 
 def load(path=None):
-    """Opens libexactsample_amd.so (or `path`) and declares its signatures."""
+    """Opens libexactsample_amd.so (or `path`) and declares its signatures.
+
+    A process must hold one HIP runtime. PyTorch-ROCm ships its own, which its
+    libraries request by an unversioned name; loaded first, ours would bind the
+    system runtime and torch would then load a second one. So torch, when
+    installed, is imported first and the library binds the runtime torch loaded.
+    """
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(str(path or os.environ.get("EXACTSAMPLE_CLIB") or _HERE / "libexactsample_amd.so"))
     lib.es_workspace_size.restype = ctypes.c_size_t
     lib.es_workspace_size.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32]
@@ -63,6 +73,8 @@ def load(path=None):
     lib.es_error_string.argtypes = [ctypes.c_int32]
     lib.es_last_hip_error.restype = ctypes.c_char_p
     lib.es_last_hip_error.argtypes = []
+    lib.es_check_gumbel.restype = ctypes.c_int32
+    lib.es_check_gumbel.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p]
     lib.es_set_split_event.restype = None
     lib.es_set_split_event.argtypes = [ctypes.c_void_p]
     lib.es_fallback_counter_offset.restype = ctypes.c_size_t

@@ -42,6 +42,10 @@ Geometry choose_geometry(int64_t rows, int64_t groups, bool large_tiles) {
 
 }  // namespace
 
+void es::note_hip_error(hipError_t err) {
+  snprintf(g_last_hip_error, sizeof(g_last_hip_error), "%s", hipGetErrorString(err));
+}
+
 extern "C" {
 
 size_t es_workspace_size(int64_t rows, int64_t vocab, int32_t reference) {
@@ -122,7 +126,7 @@ int32_t es_launch(const es_arguments* args, void* stream_ptr) {
     default: err = es::launch_dtype<ES_BF16>(a, pl, geo.g, vectorizable<ES_BF16>(a), stream, g_split_event); break;
   }
   if (err != hipSuccess) {
-    snprintf(g_last_hip_error, sizeof(g_last_hip_error), "%s", hipGetErrorString(err));
+    es::note_hip_error(err);
     return ES_ERR_LAUNCH;
   }
   return ES_SUCCESS;

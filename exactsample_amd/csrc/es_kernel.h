@@ -1,26 +1,32 @@
 // exactsample_amd device code: sampling and speculative-draft verification on gfx950.
 //
-// One launch per call (es_launch). The grid has two kinds of 256-thread blocks:
+// Two kernels per call (es_launch), on the caller's stream:
 //
+//  es_main, a grid of 256-thread blocks of two kinds:
 //  * request blocks (the first ceil(R / 256)): validate each request's
-//    metadata and write the outputs of every request that fails it
-//    (reference: csrc/verify/verify.cu:6-56, initialize);
-//  * slice blocks (rows x slices): one pass over a slice of a row held in
-//    registers: validation (NaN/+inf anywhere), the valid count, the two
-//    largest valid logits, and, for rows a list can finish, every valid logit
-//    at or above a threshold chosen so that the slice's top L are stored
+//    metadata and write the outputs of every request that fails it; they also
+//    clear the call's header words (reference: csrc/verify/verify.cu:6-56,
+//    initialize);
+//  * slice blocks (rows x slices, one register tile of up to 16 x 4 logits per
+//    thread): one pass over a slice of a row: validation (NaN/+inf anywhere),
+//    the valid count, the two largest valid logits and, for rows a list can
+//    finish, every valid logit at or above a threshold chosen so that the
+//    slice's top L are stored, or exactly its first L after a radix cut
 //    (reference: fused.cuh:409-519 row_stats, :686-798 row_hist/row_gather).
-//    The last slice block of a row to arrive merges the slices in slice order
-//    and finishes the row:
-//      - failed and greedy rows directly;
-//      - list rows (top-k <= list_max, small top-p nuclei) from the merged
-//        candidates, in FP64 with the oracle's formulas, the whole block
-//        working (reference: fused.cuh:1250-1412);
-//      - every other row on the full-row path, re-reading the row: exact
-//        radix cuts, exact top-p boundary, certified FP32 draws with FP64
-//        rescoring (reference: fused.cuh:1446-1810).
-//    The block that completes a request's last row commits the request
-//    (reference: verify.cu:169-217, finalize).
+//    Each slice writes a SlicePart with plain stores; the row's first slice
+//    also records the row's resolved request parameters.
+//
+//  es_finish, one block per row (the kernel boundary makes every slice's
+//  stores visible): merges the slices in slice order and finishes the row:
+//    - failed and greedy rows directly;
+//    - top-k rows from the union of the slices' candidates in one wave, in FP64
+//      with the oracle's formulas (reference: fused.cuh:1250-1412);
+//    - other list rows (small top-p nuclei) with the whole block;
+//    - every other row on the full-row path, re-reading the row: exact radix
+//      cuts, exact top-p boundary, certified FP32 draws with FP64 rescoring
+//      (reference: fused.cuh:1446-1810).
+//  The block that completes a request's last row commits the request
+//  (reference: verify.cu:169-217, finalize).
 //
 // Results never depend on the slice count, the slot or the arrival order:
 // merges run in slice order, candidate sets are exact up to a recorded
@@ -549,10 +555,9 @@ __device__ __forceinline__ void finalize_request(const es_arguments& a, int64_t 
   }
 }
 
-// The call's FP64 recomputation count, workspace word 1: zeroed by the first
-// kernel, then added to by the full-row kernel (which runs after it): its
-// block 0 adds what the rows finished in the first kernel recorded, and each
-// full-row block adds its own row's.
+// The call's FP64 recomputation count, workspace word 1: cleared by es_main's
+// request blocks, then added to by each es_finish block that needed one (the
+// kernel boundary orders the two).
 __device__ __forceinline__ void add_fallbacks(const es_arguments& a, unsigned n) {
   if (n) atomicAdd(reinterpret_cast<unsigned*>(a.workspace) + 1, n);
 }
@@ -2318,13 +2323,18 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments a, Plan pl) {
 namespace es {
 template <int DT, bool VEC, int G>
 hipError_t launch_main(const es_arguments& a, const Plan& pl, hipStream_t stream, hipEvent_t split) {
+  // hipLaunchKernel reports this launch's own error (a stale error of the
+  // caller's thread is neither returned nor cleared).
+  es_arguments args = a;
+  Plan plan = pl;
+  void* params[] = {&args, &plan};
   const unsigned blocks = unsigned(pl.req_blocks + a.rows * pl.slices);
-  hipLaunchKernelGGL((es_main<DT, VEC, G>), dim3(blocks), dim3(BLOCK), 0, stream, a, pl);
-  hipError_t err = hipGetLastError();
+  hipError_t err = hipLaunchKernel(reinterpret_cast<const void*>(&es_main<DT, VEC, G>), dim3(blocks), dim3(BLOCK),
+                                   params, 0, stream);
   if (err == hipSuccess && split) err = hipEventRecord(split, stream);
   if (err != hipSuccess || a.rows == 0) return err;
-  hipLaunchKernelGGL((es_finish<DT, VEC>), dim3(unsigned(a.rows)), dim3(BLOCK), 0, stream, a, pl);
-  return hipGetLastError();
+  return hipLaunchKernel(reinterpret_cast<const void*>(&es_finish<DT, VEC>), dim3(unsigned(a.rows)), dim3(BLOCK),
+                         params, 0, stream);
 }
 
 // Register tiles built for a dtype: the host picks one of them per call.

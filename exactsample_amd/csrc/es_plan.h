@@ -6,6 +6,9 @@
 
 namespace es {
 
+// Records a HIP error's text for es_last_hip_error (this thread).
+void note_hip_error(hipError_t err);
+
 // Launch geometry chosen by the host for a call.
 struct Plan {
   int32_t slices;        // blocks per row

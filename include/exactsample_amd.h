@@ -101,6 +101,18 @@ const char* es_last_hip_error(void);
  * off. Recording adds a stream marker, so leave it off outside measurement. */
 void es_set_split_event(void* event);
 
+/* Device self-test with no counterpart in the reference's API; it makes, on this
+ * GPU and with this library's build, the checks of the reference's
+ * tests/exhaustive/gumbel_bound.cu:33-78 for the FP32 Gumbel noise the certified
+ * draws use: over words [first_word, first_word + count) of the 2^32 Philox
+ * words, |gumbel32 - G| <= 2^-19 (1 + |G|), the cheap screen >= G, and
+ * G < 22.875, where G = -log(-log u) in FP64. `report` is 8 device uint64 words
+ * (8-byte aligned), overwritten: words checked, error-bound violations,
+ * screen violations, range violations, largest error / bound (FP64 bits),
+ * then the smallest screen margin, largest G and smallest G as order keys
+ * (key k: FP64 bits k & ~2^63 if k >= 2^63, else ~k). Enqueued on `stream`. */
+int32_t es_check_gumbel(uint64_t first_word, uint64_t count, uint64_t* report, void* stream);
+
 /* Offset of the FP64 recomputation counter in the workspace (a uint32 written by
  * each call; read it after the call completes). Replaces workspace word 1 read at
  * python/exactsample/cuda.py:109-114. */
