@@ -92,7 +92,94 @@ def config4(seed=4, requests=64, drafts=4):
     return dict(rows=rows, offsets=offsets, ids=ids, keys=keys, params=QWEN, mode="ratio")
 
 
+def _keys(rng, seed, requests, rows):
+    return dict(seed=seed + np.arange(requests, dtype=np.int64), stream=np.arange(requests, dtype=np.int64),
+                positions=rng.integers(0, 4096, size=rows).astype(np.int64))
+
+
+def config1(seed=1, requests=8):
+    """8 requests, one row each, temperature 1.0 and no other filter."""
+    rng = np.random.default_rng(seed)
+    rows = peaked_rows(rng, requests)
+    return dict(rows=rows, offsets=np.arange(requests + 1, dtype=np.int64),
+                ids=np.full((requests, 1), -1, dtype=np.int64), keys=_keys(rng, seed, requests, requests),
+                params=dict(temperature=1.0, top_k=0, top_p=1.0, min_p=0.0), mode="ratio")
+
+
+def config3(seed=3, requests=128, filt="top_p"):
+    """Rows of flatness sigma ~ U(0.5, 4) at T=0.7 with top-p 0.9 (or min-p 0.05).
+
+    Every tenth row is built so that FP32 cannot settle the threshold: for
+    top-p, ten tokens at logit 0 and the rest at or below -100, so the target
+    0.9 * 10 equals a prefix sum exactly; for min-p, one token whose weight is
+    within a relative 1e-9 of 0.05 (above on even rows, below on odd ones).
+    """
+    rng = np.random.default_rng(seed)
+    rows = peaked_rows(rng, requests, sigma=(0.5, 4.0))
+    for r in range(0, requests, 10):
+        if filt == "top_p":
+            row = np.full(VOCAB, -100.0, np.float32) - rng.uniform(0, 20, VOCAB).astype(np.float32)
+            row[rng.choice(VOCAB, 10, replace=False)] = 0.0
+        else:
+            row = rows[r] - rows[r].max()
+            side = 1 + (1e-9 if (r // 10) % 2 == 0 else -1e-9)
+            row[int(rng.integers(VOCAB))] = np.float32(0.7 * np.log(0.05 * side))
+            row[int(rng.integers(VOCAB))] = 0.0
+        rows[r] = row
+    params = dict(temperature=0.7, top_k=0, top_p=0.9 if filt == "top_p" else 1.0,
+                  min_p=0.05 if filt == "min_p" else 0.0)
+    return dict(rows=rows, offsets=np.arange(requests + 1, dtype=np.int64),
+                ids=np.full((requests, 1), -1, dtype=np.int64), keys=_keys(rng, seed, requests, requests),
+                params=params, mode="ratio")
+
+
+def config5(seed=5, requests=256, variant="full_ratio"):
+    """Ragged verification: draft lengths ~ U{0..7}, a mask allowing a random
+    10% of each row, filters by request {temperature only, top-k 4096, top-p
+    0.99, min-p 0.02} at T=1, and requests in a permuted slot order.
+
+    variant "full_ratio": full proposals q = log softmax(target + N(0, 1)) in
+    fp32, drafts drawn from q, ratio mode; "one_hot_coupled": the same drafts
+    as one-hot in coupled mode; "full_coupled": the literal combination, which
+    the contract makes INVALID_INPUT for every request with drafts.
+    """
+    rng = np.random.default_rng(seed)
+    drafts = rng.integers(0, 8, size=requests)
+    order = rng.permutation(requests)
+    drafts = drafts[order]
+    offsets = np.concatenate([[0], np.cumsum(drafts + 1)]).astype(np.int64)
+    n = int(offsets[-1])
+    rows = peaked_rows(rng, n)
+    noisy = rows + rng.standard_normal(rows.shape).astype(np.float32)
+    q = (noisy - noisy.max(axis=1, keepdims=True)).astype(np.float32)
+    q = (q - np.log(np.exp(q.astype(np.float64)).sum(axis=1, keepdims=True))).astype(np.float32)
+    ids = np.full((requests, 7), -1, dtype=np.int64)
+    for r in range(requests):
+        for d in range(int(drafts[r])):
+            g = -np.log(-np.log(rng.random(VOCAB)))
+            ids[r, d] = int(np.argmax(q[offsets[r] + d] + g))
+    allowed = rng.random((n, VOCAB)) < 0.1
+    kinds = order % 4
+    params = dict(temperature=[1.0] * requests,
+                  top_k=[4096 if k == 1 else 0 for k in kinds],
+                  top_p=[0.99 if k == 2 else 1.0 for k in kinds],
+                  min_p=[0.02 if k == 3 else 0.0 for k in kinds],
+                  draft_kind=["one_hot" if variant == "one_hot_coupled" else "full"] * requests)
+    return dict(rows=rows, offsets=offsets, ids=ids, keys=_keys(rng, seed, requests, n), params=params,
+                mode="ratio" if variant == "full_ratio" else "coupled", allowed=allowed,
+                draft_logits=None if variant == "one_hot_coupled" else q)
+
+
 CELLS = {"128x1": config2, "64x5": config4}
+
+
+def packed_mask(allowed):
+    """A boolean [rows, V] array as int32 words: bit t % 32 of word t // 32."""
+    rows, vocab = allowed.shape
+    padded = np.zeros((rows, -(-vocab // 32) * 32), dtype=bool)
+    padded[:, :vocab] = allowed
+    return np.packbits(padded.reshape(rows, -1, 32), axis=-1, bitorder="little").view("<u4").reshape(
+        rows, -1).view(np.int32)
 
 
 def device_args(work, device="cuda"):
@@ -102,20 +189,29 @@ def device_args(work, device="cuda"):
     requests = len(work["offsets"]) - 1
     p = work["params"]
 
-    def full(value, dtype):
-        return torch.full((requests,), value, dtype=dtype, device=device)
+    def per_request(value, dtype):
+        if np.ndim(value) == 0:
+            return torch.full((requests,), value, dtype=dtype, device=device)
+        return torch.as_tensor(np.asarray(value), dtype=dtype, device=device)
 
-    params = CudaRequestParams(full(p["temperature"], torch.float64), full(p["top_k"], torch.int64),
-                               full(p["top_p"], torch.float64), full(p["min_p"], torch.float64),
-                               full(0, torch.int64))
+    kinds = p.get("draft_kind", "one_hot")
+    kinds = [kinds] * requests if isinstance(kinds, str) else list(kinds)
+    params = CudaRequestParams(per_request(p["temperature"], torch.float64), per_request(p["top_k"], torch.int64),
+                               per_request(p["top_p"], torch.float64), per_request(p["min_p"], torch.float64),
+                               per_request([0 if k == "one_hot" else 1 for k in kinds], torch.int64))
     rng = CudaRngKey(torch.as_tensor(work["keys"]["seed"], device=device),
                      torch.as_tensor(work["keys"]["stream"], device=device),
                      torch.as_tensor(work["keys"]["positions"], device=device))
     logits = torch.as_tensor(work["rows"], device=device)
     w = plan(logits.shape[0], requests, work["ids"].shape[1], logits.shape[1])
-    return dict(target_logits=logits, cu_rows=torch.as_tensor(work["offsets"], device=device),
+    args = dict(target_logits=logits, cu_rows=torch.as_tensor(work["offsets"], device=device),
                 draft_ids=torch.as_tensor(work["ids"], device=device), params=params, rng=rng, plan=w,
                 out=w.allocate_output())
+    if work.get("allowed") is not None:
+        args["mask"] = torch.as_tensor(packed_mask(work["allowed"]), device=device)
+    if work.get("draft_logits") is not None:
+        args["draft_logits"] = torch.as_tensor(work["draft_logits"], device=device)
+    return args
 
 
 def algorithmic_bytes(work):

@@ -140,6 +140,11 @@ __device__ __forceinline__ SlicePart* slice_parts(const es_arguments& a, int64_t
 template <class W> __device__ __forceinline__ Cand<W>* candidates(const es_arguments& a, int64_t row) {
   return reinterpret_cast<Cand<W>*>(row_region(a, row) + OFF_CAND);
 }
+// A stream row's slice keeps its pick where a list row keeps candidates.
+struct Pick;
+template <class W> __device__ __forceinline__ Pick* slice_pick(const es_arguments& a, int64_t row, int slice, int cap) {
+  return reinterpret_cast<Pick*>(candidates<W>(a, row) + int64_t(slice) * cap);
+}
 
 // ---------------------------------------------------------------------------
 // Metadata (reference verify.cu:6-40; oracle reference.py:177-196).
@@ -248,6 +253,11 @@ __device__ __forceinline__ bool arrive(uint32_t* counter, uint32_t expected, int
 
 // ---------------------------------------------------------------------------
 // Shared memory of a block (one union; each phase uses one member).
+// A certified FP32 Gumbel-max: the best score mid (higher, then lower ID),
+// an interval [lo, hi] holding its exact score, and a bound on every other
+// candidate's score.
+struct Pick { float mid, lo, hi, others; int id; };
+
 template <class W> struct Shared {
   union {
     struct {
@@ -291,6 +301,11 @@ template <class W> struct Shared {
   W st_max[WAVES], st_thr[WAVES];
   int st_id[WAVES], st_valid[WAVES], st_bad[WAVES];
   int appended;
+  // Stream rows: block merges of picks, the merged pick and the slices to scan again.
+  Pick picks[WAVES];
+  double sp_mid, sp_lo, sp_hi, sp_others;
+  int sp_id;
+  unsigned long long sp_rescan;
   // The merge wave's decision, broadcast to the block.
   RowResult wres;
   int wroute, wfallbacks, wdone;
@@ -306,6 +321,17 @@ struct Params {
   int draft_row, verify, coupled, full_q, draft_id;
   RngAddr rng;
 };
+
+// A stream row samples from every kept token in one streaming pass: a
+// positive temperature, no top-k cut, top-p 1 and no full proposal; min-p
+// rows qualify unless the ratio test needs their kept mass.
+__device__ __forceinline__ bool stream_row(const Params& p, int64_t vocab) {
+  return p.temperature > 0 && !p.full_q && !(p.top_p < 1) && (p.top_k == 0 || p.top_k >= vocab) &&
+         !(p.verify && !p.coupled && p.min_p > 0);
+}
+// The draw a stream row needs: the residual (substream 2, draft excluded) for
+// a draft row in ratio mode, the sample (substream 0) otherwise.
+__device__ __forceinline__ uint32_t stream_sub(const Params& p) { return p.verify && !p.coupled ? 2u : 0u; }
 static_assert(sizeof(Params) <= ROW_META_BYTES, "Params fits the row's meta area");
 __device__ __forceinline__ Params* row_meta(const es_arguments& a, int64_t row) {
   return reinterpret_cast<Params*>(row_region(a, row) + OFF_META);
@@ -456,9 +482,9 @@ struct ListPlan {
   bool sorted_list;  // a top-k row (k <= 64, within the slice capacity) finished by one wave
   bool need_topp;    // a top-p list: the slices also sum their kept weights
 };
-__device__ __forceinline__ ListPlan list_plan(const Params& p, int list_max, int cap) {
+__device__ __forceinline__ ListPlan list_plan(const Params& p, int list_max, int cap, int64_t vocab) {
   ListPlan lp{0, 0, false, false};
-  if (p.temperature > 0 && list_max > 0 && !p.full_q) {
+  if (p.temperature > 0 && list_max > 0 && !p.full_q && !stream_row(p, vocab)) {
     if (p.top_k >= 1 && p.top_k <= list_max) lp.need = int(p.top_k);
     else if (p.top_p < 1 && p.min_p == 0) lp.need = TOPP_SLICE_NEED;
     else lp.need = -1;
@@ -1615,6 +1641,204 @@ template <int DT, bool VEC> struct FullRow {
 };
 
 // ---------------------------------------------------------------------------
+// The streaming draw of stream rows (reference: fused.cuh:532-681 row_scan and
+// its Pick merge :301-314).
+__device__ __forceinline__ Pick pick_none() { return Pick{-INFINITY, -INFINITY, -INFINITY, -INFINITY, INT_MAX}; }
+__device__ __forceinline__ Pick pick_join(Pick x, Pick y) {
+  const bool yw = y.mid > x.mid || (y.mid == x.mid && y.id < x.id);
+  Pick w = yw ? y : x;
+  const Pick l = yw ? x : y;
+  w.others = fmaxf(fmaxf(x.others, y.others), l.hi);
+  return w;
+}
+template <class SH> __device__ __forceinline__ Pick block_pick(Pick pk, SH& sh) {
+  pk = wave_all(pk, pick_join, pick_none());
+  __syncthreads();
+  if (lane_id() == 0) sh.picks[wave_id()] = pk;
+  __syncthreads();
+  Pick r = sh.picks[0];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) r = pick_join(r, sh.picks[w]);
+  __syncthreads();
+  return r;
+}
+
+// A thread's Kahan sum of exp(x) over kept tokens with x >= SUM_PRUNE, its
+// error bound term, and the count of kept tokens below SUM_PRUNE.
+struct KahanSum {
+  float s = 0.f, c = 0.f, e = 0.f;
+  int pruned = 0;
+  __device__ __forceinline__ void add(float x) {
+    if (!(x >= SUM_PRUNE)) { ++pruned; return; }
+    const float w = expf(x), d = w - c, t = s + d;
+    c = (t - s) - d;
+    s = t;
+    e += w * (X_ERR * (1.f + fabsf(x)));
+  }
+};
+
+// One group of four tokens into a thread's certified pick: tokens whose bit
+// is set in `bits`, above -inf, not `excluded` and passing keep(v, x), scored
+// x + G(word(sub, t)) with x = tp.x32(v). A token whose score bound stays
+// under `bar` (the floor, then the thread's best lower bound) needs no Philox
+// word; one Philox call serves the group's four tokens. With SUM, every such
+// token (the excluded one too) also goes into `sum`.
+template <bool SUM, class W, class Keep>
+__device__ __forceinline__ void pick_group(int g, const W (&x)[4], uint32_t bits, const Temp<W>& tp,
+                                           const RngAddr& rng, uint32_t sub, int excluded, Keep&& keep, Pick& best,
+                                           float& bar, KahanSum* sum) {
+  float xs[4];
+  uint32_t live = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const W v = x[j];
+    xs[j] = tp.x32(v);
+    const bool ok = ((bits >> j) & 1u) && v > neg_inf<W>() && keep(v, xs[j]);
+    if constexpr (SUM) {
+      if (ok) sum->add(xs[j]);
+    }
+    if (!ok || 4 * g + j == excluded) continue;
+    const float ub = xs[j] + GUMBEL_MAX + SCORE_ERR * (1.f + fabsf(xs[j]) + GUMBEL_MAX);
+    if (ub < bar) {
+      best.others = fmaxf(best.others, ub);
+      continue;
+    }
+    live |= 1u << j;
+  }
+  if (!live) return;
+  const Words w4 = philox(rng.seed, rng.stream, rng.position, sub, uint32_t(g));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (!((live >> j) & 1u)) continue;
+    const uint32_t w = w4.w[j];
+    const float gb = gumbel_upper(w);
+    const float ub2 = xs[j] + gb + SCORE_ERR * (1.f + fabsf(xs[j]) + fabsf(gb));
+    if (ub2 < bar) {
+      best.others = fmaxf(best.others, ub2);
+      continue;
+    }
+    const float G = gumbel32(w), sc = xs[j] + G, e = SCORE_ERR * (1.f + fabsf(xs[j]) + fabsf(G));
+    const int t = 4 * g + j;
+    if (sc > best.mid || (sc == best.mid && t < best.id)) {
+      best.others = fmaxf(best.others, best.hi);
+      best = Pick{sc, sc - e, sc + e, best.others, t};
+    } else {
+      best.others = fmaxf(best.others, sc + e);
+    }
+    bar = fmaxf(bar, best.lo - PRUNE_MARGIN);
+  }
+}
+
+// The thread's certified pick over the allowed tokens of groups [g_begin,
+// g_end) read from memory, B groups in flight per thread (thread k takes
+// g_begin + k, + BLOCK, ...).
+template <int B, bool SUM, int DT, bool VEC, class Keep>
+__device__ __forceinline__ Pick range_pick(const es_arguments& a, int64_t row, const RowView<DT, VEC>& view,
+                                           int g_begin, int g_end, const Temp<typename Ty<DT>::W>& tp,
+                                           const RngAddr& rng, uint32_t sub, int excluded, float floor, Keep&& keep,
+                                           KahanSum* sum) {
+  using W = typename Ty<DT>::W;
+  Pick best = pick_none();
+  float bar = floor - PRUNE_MARGIN;
+  for (int base = g_begin + int(threadIdx.x); base < g_end; base += B * BLOCK) {
+    W x[B][4];
+    uint32_t mb[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int g = base + u * BLOCK;
+      view.load(min(g, g_end - 1), x[u]);
+      mb[u] = g < g_end ? group_bits(a, row, g) : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u) pick_group<SUM>(base + u * BLOCK, x[u], mb[u], tp, rng, sub, excluded, keep, best, bar, sum);
+  }
+  return best;
+}
+
+// A stream row's slice: its certified draw over the slice's tokens that may
+// be kept, read again from memory (cache hits), stored where a list row keeps
+// candidates (reference: fused.cuh:532-681 row_scan). Scores are relative to
+// a reference maximum: the slice's, or for a min-p row the largest slice
+// maximum of the row published so far, a lower bound on the row maximum, so
+// the tokens that may be kept against it (valid, not certainly below min-p or
+// underflowing) are a superset of the kept ones. A min-p slice whose pick
+// falls under the threshold of a larger maximum published meanwhile draws
+// again against that one. The merge settles which pick is kept, exactly, and
+// scans again any slice whose pick is not. Ratio rows also sum their kept
+// weights (relative to the slice maximum).
+struct SliceDraw { double sum, err, mref; int pruned; };
+template <int DT, bool VEC, class W>
+__device__ __forceinline__ SliceDraw slice_draw(const es_arguments& a, int64_t row, int slice, Params p,
+                                             const RowView<DT, VEC>& view, int g0, int g1, double smax, int first_id,
+                                             int cap_slice, Shared<W>& sh) {
+  constexpr int B = 4;  // groups in flight per thread
+  const int tid = threadIdx.x;
+  load_row_rng(a, row, &p);
+  const uint32_t sub = stream_sub(p);
+  const int excluded = sub == 2u ? p.draft_id : -1;
+  unsigned long long* key = &counters(a, row)->max_key;
+  auto published = [&]() {
+    if (tid == 0) sh.dred[0] = key_value(uint64_t(__hip_atomic_load(key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
+    __syncthreads();
+    const double m = sh.dred[0];
+    __syncthreads();
+    return m;
+  };
+  double mref = smax;
+  if (p.min_p > 0) {
+    if (tid == 0) atomicMax(key, (unsigned long long)order_key(smax));
+    mref = published();
+  }
+  Temp<W> ts;
+  ts.init(mref, p.temperature, p.min_p);
+  auto maybe_kept = [&](W, float x) { return x > -746.5f && x >= ts.ln_min_p - (X_ERR * fabsf(x) + ts.min_p_tol); };
+  // The floor: the slice maximum's own score, when it may be drawn.
+  auto floor_of = [&]() {
+    if (tid == 0) {
+      float f = -INFINITY;
+      const float x = ts.x32(W(smax));
+      if (first_id != excluded && maybe_kept(W(smax), x)) {
+        const float g = gumbel32(word_of(p.rng, sub, uint32_t(first_id)));
+        f = x + g - SCORE_ERR * (1.f + fabsf(x) + fabsf(g));
+      }
+      sh.fred[0] = f;
+    }
+    __syncthreads();
+    const float f = sh.fred[0];
+    __syncthreads();
+    return f;
+  };
+  SliceDraw out{0.0, 0.0, mref, 0};
+  Pick pk;
+  if (sub == 2u) {
+    // Ratio rows (never min-p ones) also sum their kept weights for the acceptance test.
+    KahanSum ks;
+    pk = range_pick<B, true>(a, row, view, g0, g1, ts, p.rng, sub, excluded, floor_of(), maybe_kept, &ks);
+    out.sum = block_all(double(ks.s) - double(ks.c), [](double x, double y) { return x + y; }, sh.dred, 0.0);
+    out.err = block_all(double(ks.e), [](double x, double y) { return x + y; }, sh.dred, 0.0);
+    out.pruned = block_all(ks.pruned, [](int x, int y) { return x + y; }, sh.ired, 0);
+    pk = block_pick(pk, sh);
+  } else {
+    pk = range_pick<B, false>(a, row, view, g0, g1, ts, p.rng, sub, excluded, floor_of(), maybe_kept, nullptr);
+    pk = block_pick(pk, sh);
+    if (p.min_p > 0 && pk.id != INT_MAX) {
+      const double m2 = published();
+      if (m2 > mref) {
+        ts.init(m2, p.temperature, p.min_p);
+        const W vp = view.value(pk.id);
+        if (!ts.kept(vp, ts.x32(vp))) {
+          out.mref = m2;
+          pk = range_pick<B, false>(a, row, view, g0, g1, ts, p.rng, sub, excluded, floor_of(), maybe_kept, nullptr);
+          pk = block_pick(pk, sh);
+        }
+      }
+    }
+  }
+  if (tid == 0) *slice_pick<W>(a, row, slice, cap_slice) = pk;
+  return out;
+}
+
+// ---------------------------------------------------------------------------
 // The slice's tokens in the register tile's order. Token (i, j) of a thread
 // is 4 * (gb + BLOCK * i) + j, so IDs rise with (i, thread, j); tokens that
 // are masked or outside the slice have the value -inf. The tile itself dies
@@ -1889,7 +2113,7 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4)))
     if (lane == 0) *row_meta(a, row) = p;
   }
   if (p.status != ES_OK) return;
-  const ListPlan lp = list_plan(p, a.list_max, pl.cap_slice);
+  const ListPlan lp = list_plan(p, a.list_max, pl.cap_slice, a.vocab);
   int need = lp.need;
   const int L = lp.L;
   const bool sorted_list = lp.sorted_list, need_topp = lp.need_topp;
@@ -2018,7 +2242,7 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4)))
   // Only groups whose maximum reaches the threshold are read again (they are
   // few: the slice's top tokens); the rest of the slice is never revisited.
   const MemVisit<DT, VEC, G> mem(a, row, view, gb, g1, pl.groups);
-  double frontier = -INFINITY, psum = 0, perr = 0;
+  double frontier = -INFINITY, psum = 0, perr = 0, tau = -INFINITY;
   int n_cand = 0, pruned = 0, fid = INT_MAX;
   if (sorted_list && need > 0) {
     // Top-k rows: every valid token >= the threshold (at least L of them),
@@ -2144,13 +2368,19 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4)))
       perr = block_all(double(e), [](double x, double y) { return x + y; }, sh.dred, 0.0);
       pruned = block_all(pr, [](int x, int y) { return x + y; }, sh.ired, 0);
     }
+  } else if (stream_row(p, a.vocab) && !bad && valid > 0) {
+    const SliceDraw sd = slice_draw<DT, VEC>(a, row, slice, p, view, g0, g1, double(smax), first_id, pl.cap_slice, sh);
+    psum = sd.sum;
+    perr = sd.err;
+    pruned = sd.pruned;
+    tau = sd.mref;
   }
   if (tid == 0) {
     SlicePart part;
     part.max_v = double(smax);
     part.second_v = -INFINITY;
     part.frontier = frontier;
-    part.tau = -INFINITY;
+    part.tau = tau;  // a stream row's reference maximum for its pick
     part.sum = psum;
     part.err = perr;
     part.max_id = first_id;
@@ -2161,6 +2391,77 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4)))
     part.flags = bad;
     slice_parts(a, row)[slice] = part;
   }
+}
+
+// ---------------------------------------------------------------------------
+// A pick with FP64 scores relative to the row maximum (slices' picks after
+// their shift).
+struct DPick { double mid, lo, hi, others; int id; };
+__device__ __forceinline__ DPick dpick_none() { return DPick{-INFINITY, -INFINITY, -INFINITY, -INFINITY, INT_MAX}; }
+__device__ __forceinline__ DPick dpick_join(DPick x, DPick y) {
+  const bool yw = y.mid > x.mid || (y.mid == x.mid && y.id < x.id);
+  DPick w = yw ? y : x;
+  const DPick l = yw ? x : y;
+  w.others = fmax(fmax(x.others, y.others), l.hi);
+  return w;
+}
+
+// Finishes a stream row from its slices' picks (merged into sh.sp_* by the
+// merge wave): scans again, exactly against the row maximum, the slices whose
+// pick is not kept, then takes the winner when its interval clears every
+// other score, and for a draft row in ratio mode settles u < min(1, p_x)
+// with the slices' kept mass (reference: fused.cuh:532-681, the last slice's
+// commit; reference.py:229-230). False when a certificate fails: the
+// full-row path then decides.
+template <int DT, bool VEC, class W>
+__device__ __forceinline__ bool stream_finish(const es_arguments& a, int64_t row, const Params& p, const Plan& pl,
+                                              Shared<W>& sh, RowResult* out, int* why) {
+  const RowView<DT, VEC> view(a.target, row, int(a.vocab));
+  Temp<W> tm;
+  tm.init(sh.maximum, p.temperature, p.min_p);
+  const uint32_t sub = stream_sub(p);
+  const int excluded = sub == 2u ? p.draft_id : -1;
+  DPick best{sh.sp_mid, sh.sp_lo, sh.sp_hi, sh.sp_others, sh.sp_id};
+  unsigned long long again = sh.sp_rescan;
+  __syncthreads();
+  while (again) {
+    const int s = __ffsll(again) - 1;
+    again &= again - 1;
+    const int gs = s * pl.gps, ge = min(gs + pl.gps, pl.groups);
+    const float floor = best.id != INT_MAX ? float(best.lo) : -INFINITY;
+    Pick r = range_pick<4, false>(a, row, view, gs, ge, tm, p.rng, sub, excluded, floor,
+                                  [&](W v, float x) { return tm.kept(v, x); }, nullptr);
+    r = block_pick(r, sh);
+    best = dpick_join(best, DPick{double(r.mid), double(r.lo), double(r.hi), double(r.others), r.id});
+  }
+  if (best.id != INT_MAX && !(best.lo > best.others)) {
+    *why = 8;  // scores too close for FP32: the full-row path rescores them in FP64
+    return false;
+  }
+  const int token = best.id == INT_MAX ? -1 : best.id;
+  if (sub != 2u) {
+    out->sample = token;
+    return true;
+  }
+  // Ratio test of the draft (one-hot q: p_x / q_x = p_x).
+  bool accept = false;
+  const int x = p.draft_id;
+  const W vx = view.value(x);
+  if (allowed(a, row, x) && vx > neg_inf<W>() && tm.kept(vx, tm.x32(vx))) {
+    const double u = uniform64(word_of(p.rng, 1u, 0u));
+    const double S = sh.sum, E = sh.err, wx = exp(tm.x64(vx));
+    const bool bounded = E >= 0 && S - E > 0;
+    const double rlo = fmin(1.0, wx / (S + E)) * (1 - 1e-12), rhi = fmin(1.0, wx / (S - E)) * (1 + 1e-12);
+    if (bounded && u < rlo) {
+      accept = true;
+    } else if (!(bounded && u >= rhi)) {
+      *why = 9;  // the acceptance needs the exact mass
+      return false;
+    }
+  }
+  out->p = accept ? 1.0 : 0.0;
+  if (!accept) out->residual = token;
+  return true;
 }
 
 // ---------------------------------------------------------------------------
@@ -2183,6 +2484,7 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments a, Plan pl) {
   const Params p = *row_meta(a, row);
   const SlotMap map(min(pl.cap_slice, WAVE * WAVE_BATCH / pl.slices));
   Cand<W> pre[WAVE_BATCH];
+  if (tid == 0) counters(a, row)->max_key = 0;  // the slices published their maxima; ready for the next call
   SlicePart q;
   q.max_v = -INFINITY; q.second_v = -INFINITY; q.frontier = -INFINITY; q.tau = -INFINITY;
   q.sum = 0; q.err = 0; q.max_id = INT_MAX; q.second_id = INT_MAX; q.valid = 0; q.n_cand = 0; q.pruned = 0; q.flags = 0;
@@ -2203,8 +2505,10 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments a, Plan pl) {
     return;
   }
   const int list_max = a.list_max;
-  const ListPlan lp = list_plan(p, list_max, pl.cap_slice);
+  const ListPlan lp = list_plan(p, list_max, pl.cap_slice, a.vocab);
   const bool sorted_list = lp.sorted_list, need_topp = lp.need_topp;
+  const bool stream = stream_row(p, a.vocab);
+  const bool stream_sum = stream && stream_sub(p) == 2u;  // the ratio test needs the kept mass
   if (wave_id() == 0) {
     if (lane < pl.slices) sh.n_cand[lane] = q.n_cand;
     struct T2d { double v1; int i1; double v2; int i2; };
@@ -2230,7 +2534,7 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments a, Plan pl) {
     // (only top-p lists carry them: need == TOPP_SLICE_NEED in the slices).
     double s_sum = 0, s_err = 0;
     int s_pr = 0;
-    if (need_topp) {
+    if (need_topp || stream_sum) {
       s_pr = q.pruned;
       if (lane < pl.slices && q.valid > 0) {
         const double shift = (t2.v1 - q.max_v) / p.temperature;
@@ -2247,6 +2551,40 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments a, Plan pl) {
       sh.valid = vsum; sh.bad = bsum; sh.frontier = fr.v; sh.frontier_id = fr.id; sh.n_cand_total = nct;
       sh.sum = s_sum;
       sh.err = s_err + s_pr * SUM_PRUNE_W + 1e-15 * s_sum;
+    }
+    if (stream && bsum == 0 && vsum > 0) {
+      // The slices' picks, shifted from slice maxima to the row maximum. A
+      // slice holds kept tokens when its maximum is kept; its pick counts
+      // when the pick itself is kept (exactly, against the row maximum), and
+      // otherwise the slice is scanned again below.
+      const RowView<DT, VEC> view(a.target, row, int(a.vocab));
+      Temp<W> tm;
+      tm.init(t2.v1, p.temperature, p.min_p);
+      DPick mine = dpick_none();
+      bool rescan = false;
+      if (lane < pl.slices && q.valid > 0) {
+        const W ms = W(q.max_v);
+        if (tm.kept(ms, tm.x32(ms))) {
+          const Pick sp = *slice_pick<W>(a, row, lane, pl.cap_slice);
+          const double shift = (t2.v1 - q.tau) / p.temperature;
+          const double eps = 1e-12 * (1.0 + shift + fabs(double(sp.mid)));
+          bool take = sp.id != INT_MAX;
+          if (take) {
+            const W vx = view.value(sp.id);
+            take = tm.kept(vx, tm.x32(vx));
+            rescan = !take;
+          }
+          if (take) mine = DPick{double(sp.mid) - shift, double(sp.lo) - shift - eps, double(sp.hi) - shift + eps,
+                                 -INFINITY, sp.id};
+          if (!rescan) mine.others = double(sp.others) - shift + eps;
+        }
+      }
+      mine = wave_all(mine, dpick_join, dpick_none());
+      const unsigned long long again = __ballot(rescan);
+      if (lane == 0) {
+        sh.sp_mid = mine.mid; sh.sp_lo = mine.lo; sh.sp_hi = mine.hi; sh.sp_others = mine.others;
+        sh.sp_id = mine.id; sh.sp_rescan = again;
+      }
     }
     // A top-k row is finished here by this wave.
     int wdone = 0;
@@ -2285,7 +2623,10 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments a, Plan pl) {
     result = sh.wres;
   } else {
     bool done = false;
-    if (sorted_list && sh.wdone < 0) {
+    if (stream) {
+      route = 5;
+      done = stream_finish<DT, VEC>(a, row, p, pl, sh, &result, &why);
+    } else if (sorted_list && sh.wdone < 0) {
       why = 7;  // a rounding the wave could not certify: the full-row path decides
     } else if (p.temperature > 0 && !p.full_q && list_max > 0) {
       const int valid_all = sh.valid;

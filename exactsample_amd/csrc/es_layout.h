@@ -49,11 +49,13 @@ struct RowState {
 };
 static_assert(sizeof(RowState) == 48, "RowState layout");
 
-// Arrival counters. slices: blocks of this row that finished the slice pass.
-// request: rows of the request completed (kept in the request's first row).
-// grid: rows completed in the call (kept in row 0).
+// request: rows of the request completed (an arrival counter, kept in the
+// request's first row). max_key: the largest slice maximum published so far
+// in this call (an order key; 0 is below every value), which min-p slices
+// read as a lower bound on the row maximum. Both are back to 0 after a call.
 struct Counters {
-  uint32_t slices, request, grid, pad;
+  uint32_t request, pad;
+  unsigned long long max_key;
 };
 
 // One slice's summary of its part of the row.
@@ -61,7 +63,7 @@ struct SlicePart {
   double max_v;      // largest valid logit in the slice, -inf if none
   double second_v;   // second in (value desc, id asc) order, -inf
   double frontier;   // largest valid logit not stored as a candidate; -inf if none, +inf if unusable
-  double tau;        // candidates are the valid logits >= tau (-inf: all of them)
+  double tau;        // a stream row's reference maximum: its pick's scores are relative to it
   double sum;        // FP32 sum of exp((l - max_v) / T) over kept tokens, for top-p lists
   double err;        // its error bound
   int32_t max_id, second_id, valid, n_cand, pruned, flags;

@@ -21,20 +21,27 @@ def _device(hip_device):
     load_library()
 
 
-def _run(work):
+def _run(work, list_max=None):
     from exactsample_amd.cuda import verify
 
     args = bench.device_args(work)
+    if list_max is not None:
+        args["plan"].list_max = list_max
     out = verify(**args, mode=work["mode"])
     keys = work["keys"]
     params = RequestParams(**work["params"])
     rng = RngKey([int(s) for s in keys["seed"]], [int(s) for s in keys["stream"]], keys["positions"])
-    expected = expected_for(args, work["offsets"], work["ids"], params=params, rng=rng, mode=work["mode"])
+    mask = None if work.get("allowed") is None else bench.packed_mask(work["allowed"])
+    expected = expected_for(args, work["offsets"], work["ids"], params=params, rng=rng, mode=work["mode"], mask=mask)
     requests = len(work["offsets"]) - 1
     for field in ("tokens", "accepted_len", "status"):
         np.testing.assert_array_equal(getattr(out, field).cpu().numpy()[:requests], getattr(expected, field),
                                       err_msg=field)
     return args
+
+
+def _routes(args):
+    return [route for route, _ in row_diagnostics(args["plan"], args["target_logits"].shape[0])]
 
 
 @pytest.mark.parametrize("cell", ["128x1", "64x5"])
@@ -96,3 +103,92 @@ def test_top_k_row_that_falls_back_to_the_full_row():
                                    params=RequestParams(top_k=64, temperature=0.8))
     routes = row_diagnostics(args["plan"], 2)
     assert all(route >= 100 for route, _ in routes), routes
+
+
+# ---- Stream rows: temperature only and min-p, drawn slice by slice. ----
+# Route 5 is the streaming draw; 100 + 8 / 9 the full-row path after a
+# certificate the streaming draw could not give (scores or the acceptance
+# too close for FP32).
+
+@pytest.mark.parametrize("list_max", [256, 0])
+def test_temperature_only_rows(list_max):
+    """Eight rows at T = 1, no other filter (the CPU-timed configuration)."""
+    args = _run(bench.config1(), list_max=list_max)
+    assert all(r == 5 for r in _routes(args)), _routes(args)
+
+
+def test_min_p_rows_with_thresholds_within_an_ulp():
+    """128 rows, T = 0.7, min-p 0.05; every tenth row holds a token whose
+    weight is within 1e-9 of the threshold (FP64 settles it)."""
+    args = _run(bench.config3(filt="min_p"))
+    assert all(r in (5, 108) for r in _routes(args)), sorted(set(_routes(args)))
+
+
+def test_top_p_rows_with_boundaries_on_a_prefix_sum():
+    """128 rows, T = 0.7, top-p 0.9; every tenth row puts the target exactly
+    on a prefix sum (ten tokens of weight 1)."""
+    _run(bench.config3(filt="top_p"))
+
+
+@pytest.mark.parametrize("mode", ["ratio", "coupled"])
+def test_temperature_only_drafts(mode):
+    """Drafted requests at T = 1: ratio rows need the slices' kept mass and
+    the residual draw (draft excluded); coupled rows the sample."""
+    rng = np.random.default_rng(31)
+    requests, drafts = 12, 3
+    work = bench.config1(seed=31, requests=requests * (drafts + 1))
+    work["offsets"] = np.arange(requests + 1, dtype=np.int64) * (drafts + 1)
+    rows = work["rows"]
+    ids = np.zeros((requests, drafts), np.int64)
+    for r in range(requests):
+        for d in range(drafts):
+            row = rows[r * (drafts + 1) + d]
+            ids[r, d] = int(np.argmax(row)) if rng.random() < 0.6 else int(rng.integers(0, rows.shape[1]))
+    work["ids"] = ids
+    work["keys"]["seed"] = work["keys"]["seed"][:requests]
+    work["keys"]["stream"] = work["keys"]["stream"][:requests]
+    work["mode"] = mode
+    args = _run(work)
+    assert all(r in (5, 108, 109) for r in _routes(args)), sorted(set(_routes(args)))
+
+
+def test_stream_scores_too_close_for_fp32_across_slices():
+    """Two tokens in different slices whose scores differ by 1e-10: the
+    streaming draw cannot certify either, and FP64 decides."""
+    from tests.gpu_helpers import run_and_compare
+    from oracle.rng import gumbel
+    import torch
+
+    seed, stream, position = 77, 4, 321
+    a_id, b_id = 1000, 100000  # in different slices
+    ga, gb = gumbel(seed, stream, position, 0, a_id), gumbel(seed, stream, position, 0, b_id)
+    for eps in (1e-10, -1e-10):
+        row = np.full((1, 151936), -1000.0)
+        row[0, a_id] = 0.0
+        row[0, b_id] = ga - gb + eps
+        out, fallbacks, args = run_and_compare(row, [0, 1], np.empty((1, 0), np.int64), dtype=torch.float64,
+                                               rng=RngKey(seed, stream, [position]))
+        assert out.tokens[0, 0].item() == (b_id if eps > 0 else a_id)
+        assert _routes(args) == [108]
+
+
+def test_min_p_picks_that_the_row_maximum_excludes():
+    """Flat rows (sigma 0.3, T = 0.5, min-p 0.4: about 200 kept tokens
+    spread over the slices). Each slice draws against its own maximum, below
+    the row's, so its pick may fall under the row's threshold: the merge then
+    scans that slice again against the row maximum."""
+    rng = np.random.default_rng(8)
+    rows = rng.normal(0.0, 0.3, size=(16, 151936)).astype(np.float32)
+    work = dict(rows=rows, offsets=np.arange(17, dtype=np.int64), ids=np.full((16, 1), -1, np.int64),
+                keys=dict(seed=np.arange(16, dtype=np.int64) + 3, stream=np.arange(16, dtype=np.int64),
+                          positions=np.arange(16, dtype=np.int64) * 7),
+                params=dict(temperature=0.5, top_k=0, top_p=1.0, min_p=0.4), mode="ratio")
+    args = _run(work)
+    assert all(r in (5, 108) for r in _routes(args)), sorted(set(_routes(args)))
+
+
+@pytest.mark.parametrize("variant", ["full_ratio", "one_hot_coupled", "full_coupled"])
+def test_ragged_masked_mixed_filters(variant):
+    """24 requests of the ragged configuration: draft lengths 0..7, a mask
+    allowing 10% of each row, mixed filters, permuted slots."""
+    _run(bench.config5(requests=24, variant=variant))
