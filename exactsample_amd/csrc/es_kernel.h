@@ -257,6 +257,14 @@ __device__ __forceinline__ bool arrive(uint32_t* counter, uint32_t expected, int
 // an interval [lo, hi] holding its exact score, and a bound on every other
 // candidate's score.
 struct Pick { float mid, lo, hi, others; int id; };
+__device__ __forceinline__ Pick pick_none() { return Pick{-INFINITY, -INFINITY, -INFINITY, -INFINITY, INT_MAX}; }
+__device__ __forceinline__ Pick pick_join(Pick x, Pick y) {
+  const bool yw = y.mid > x.mid || (y.mid == x.mid && y.id < x.id);
+  Pick w = yw ? y : x;
+  const Pick l = yw ? x : y;
+  w.others = fmaxf(fmaxf(x.others, y.others), l.hi);
+  return w;
+}
 
 template <class W> struct Shared {
   union {
@@ -1104,12 +1112,26 @@ __device__ __forceinline__ int wave_topk(const es_arguments& a, int64_t row, con
   }
   const bool kept = lane < count;
   const double pr = kept ? wk / den : 0.0;
-  // Gumbel-argmax over kept tokens with positive probability, lowest ID on ties.
+  // Gumbel-argmax over kept tokens with positive probability, lowest ID on
+  // ties. The scores log(p) + G differ from x + G by the common -log(den), so
+  // an FP32 x + G with its certified bound decides unless two scores are
+  // within FP32 error; then the FP64 scores decide.
   auto draw = [&](uint32_t sub, int excluded) {
+    const bool in = kept && pr > 0 && id != excluded;
+    const uint32_t word = word_of(p.rng, sub, uint32_t(in ? id : 0));
+    Pick pk = pick_none();
+    if (in) {
+      const float x = float((double(v) - M) / T), g = gumbel32(word), sc = x + g;
+      const float e = SCORE_ERR * (1.f + fabsf(x) + fabsf(g));
+      pk = Pick{sc, sc - e, sc + e, -INFINITY, id};
+    }
+    pk = wave_all(pk, pick_join, pick_none());
+    if (pk.id == INT_MAX) return -1;
+    if (pk.lo > pk.others) return pk.id;
     double s = -INFINITY;
     int sid = INT_MAX;
-    if (kept && pr > 0 && id != excluded) {
-      s = log(pr) + gumbel64(word_of(p.rng, sub, uint32_t(id)));
+    if (in) {
+      s = log(pr) + gumbel64(word);
       sid = id;
     }
     struct SI { double s; int id; };
@@ -1643,14 +1665,6 @@ template <int DT, bool VEC> struct FullRow {
 // ---------------------------------------------------------------------------
 // The streaming draw of stream rows (reference: fused.cuh:532-681 row_scan and
 // its Pick merge :301-314).
-__device__ __forceinline__ Pick pick_none() { return Pick{-INFINITY, -INFINITY, -INFINITY, -INFINITY, INT_MAX}; }
-__device__ __forceinline__ Pick pick_join(Pick x, Pick y) {
-  const bool yw = y.mid > x.mid || (y.mid == x.mid && y.id < x.id);
-  Pick w = yw ? y : x;
-  const Pick l = yw ? x : y;
-  w.others = fmaxf(fmaxf(x.others, y.others), l.hi);
-  return w;
-}
 template <class SH> __device__ __forceinline__ Pick block_pick(Pick pk, SH& sh) {
   pk = wave_all(pk, pick_join, pick_none());
   __syncthreads();
