@@ -22,22 +22,20 @@ template <int DT> bool vectorizable(const es_arguments& a) {
   return vectorizable_matrix(a, a.target) && vectorizable_matrix(a, a.draft);
 }
 
-// Per-thread register tile (groups of four) and slices per row. Prefer the
-// largest tile that still gives enough blocks to fill 256 CUs.
+// Per-thread register tile (groups of four) and slices per row. For lists
+// (top-k, top-p) the largest tile wins at every batch size measured (1 to 320
+// rows of V = 151,936): more, smaller slices cost more in the finishing
+// kernel's merge than they gain in parallelism. A call whose caller promises
+// no list rows (list_max 0) and that would not fill the device's CUs with
+// 16-group slices takes the 4-group tile: streaming draws then spread their
+// Philox work over four times the blocks. Strided rows, f16 and f64 always
+// use the 4-group tile.
 struct Geometry { int g, slices; };
-Geometry choose_geometry(int64_t rows, int64_t groups, bool large_tiles) {
-  const int large[] = {16, 8, 4};
-  const int small[] = {4, 4, 4};  // strided rows, f16 and f64 use the 4-group tile only
-  const int* options = large_tiles ? large : small;
-  Geometry best{options[0], int((groups + int64_t(options[0]) * kBlock - 1) / (int64_t(options[0]) * kBlock))};
-  for (int k = 0; k < 3; ++k) {
-    const int g = options[k];
-    const int64_t s = (groups + int64_t(g) * kBlock - 1) / (int64_t(g) * kBlock);
-    if (s > es::MAX_SLICES) break;
-    best = Geometry{g, int(s)};
-    if (rows * s >= 1024) break;
-  }
-  return best;
+Geometry choose_geometry(int64_t rows, int64_t groups, bool large_tiles, int32_t list_max) {
+  auto slices_of = [&](int g) { return int((groups + int64_t(g) * kBlock - 1) / (int64_t(g) * kBlock)); };
+  const int s16 = slices_of(16);
+  const int g = large_tiles && (list_max > 0 || rows * s16 >= 256) ? 16 : 4;
+  return Geometry{g, slices_of(g)};
 }
 
 }  // namespace
@@ -104,7 +102,7 @@ int32_t es_launch(const es_arguments* args, void* stream_ptr) {
   const int64_t groups = (a.vocab + 3) / 4;
   const bool large_tiles = (a.target.dtype == ES_F32 || a.target.dtype == ES_BF16) &&
                            vectorizable_matrix(a, a.target) && vectorizable_matrix(a, a.draft);
-  const Geometry geo = choose_geometry(a.rows, groups, large_tiles);
+  const Geometry geo = choose_geometry(a.rows, groups, large_tiles, a.list_max);
   es::Plan pl{};
   pl.groups = int(groups);
   pl.req_blocks = int((a.requests + kBlock - 1) / kBlock);

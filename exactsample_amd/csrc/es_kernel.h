@@ -2692,21 +2692,13 @@ hipError_t launch_main(const es_arguments& a, const Plan& pl, hipStream_t stream
                          params, 0, stream);
 }
 
-// Register tiles built for a dtype: the host picks one of them per call.
-template <int DT> struct Tiles;
-template <> struct Tiles<ES_F32> { static constexpr int n = 3; static constexpr int g[3] = {16, 8, 4}; };
-template <> struct Tiles<ES_BF16> { static constexpr int n = 3; static constexpr int g[3] = {16, 8, 4}; };
-template <> struct Tiles<ES_F16> { static constexpr int n = 1; static constexpr int g[3] = {4, 4, 4}; };
-template <> struct Tiles<ES_F64> { static constexpr int n = 1; static constexpr int g[3] = {4, 4, 4}; };
-
-// Contiguous rows aligned to a group of four use vector loads; any other
-// layout uses element loads with the smallest tile.
+// Contiguous rows aligned to a group of four use vector loads and, for f32
+// and bf16, the 16-group tile; any other layout or dtype uses the 4-group tile.
 template <int DT>
 hipError_t launch_dtype(const es_arguments& a, const Plan& pl, int g, bool vec, hipStream_t stream, hipEvent_t split) {
   if (!vec) return launch_main<DT, false, 4>(a, pl, stream, split);
-  if constexpr (Tiles<DT>::n == 3) {
+  if constexpr (DT == ES_F32 || DT == ES_BF16) {
     if (g == 16) return launch_main<DT, true, 16>(a, pl, stream, split);
-    if (g == 8) return launch_main<DT, true, 8>(a, pl, stream, split);
   }
   return launch_main<DT, true, 4>(a, pl, stream, split);
 }

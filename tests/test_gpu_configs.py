@@ -1,8 +1,7 @@
 """GPU parity at the benchmark's shapes (V = 151,936, 128 and 320 rows).
 
-These batches are large enough for the 16-group register tile and ten slices
-per row, the geometry the benchmark measures; the smaller tests above run the
-4-group tile. Each is checked token-for-token against the FP64 oracle, and the
+Rows of this vocabulary take ten slices of the 16-group register tile, the
+geometry the benchmark measures. Each is checked token-for-token against the FP64 oracle, and the
 list finish must settle every row without an FP64 fallback.
 """
 import numpy as np
@@ -89,20 +88,26 @@ def test_greedy_and_plain_temperature_rows():
     np.testing.assert_array_equal(out.tokens.cpu().numpy()[:128], expected.tokens)
 
 
-def test_top_k_row_that_falls_back_to_the_full_row():
-    """A flat row with k = 64 over 38 slices: the candidate union (38 x 64
-    tokens) exceeds what the wave and the block list take, so the row is
-    finished on the full-row path, which needs the row's greedy token (found
-    by the merge wave, since slices of top-k rows do not track it)."""
+def test_top_k_union_beyond_the_merge_wave():
+    """A top-k 64 row whose candidate union (792 tokens) is more than the merge
+    wave takes (512): nine slices each hold 88 tokens at 1.5, 22 in every wave
+    (one per other thread), so each slice's threshold is 1.5 and it stores
+    all 88. The whole block finishes the row as a list instead; it needs the
+    row's greedy token, which the merge wave finds (slices of top-k rows do
+    not track it)."""
     import torch
     from tests.gpu_helpers import run_and_compare
 
-    rows = np.zeros((2, 151936), np.float32)
-    rows[1, 7777] = 0.5  # a single maximum away from token 0
-    out, _, args = run_and_compare(rows, [0, 1, 2], np.empty((2, 0), np.int64), dtype=torch.float32,
-                                   params=RequestParams(top_k=64, temperature=0.8))
+    vocab, tile = 151936, 16 * 256  # groups per slice of the 16-group tile
+    rows = np.zeros((2, vocab), np.float32)
+    threads = (64 * np.arange(4)[:, None] + 2 * np.arange(22)[None, :]).ravel()  # 22 per wave
+    for s in range(1, 10):
+        rows[:, 4 * (s * tile + threads)] = 1.5
+    rows[:, 7777] = 2.0  # the maximum, alone
+    out, fallbacks, args = run_and_compare(rows, [0, 1, 2], np.empty((2, 0), np.int64), dtype=torch.float32,
+                                           params=RequestParams(top_k=64, temperature=0.8))
     routes = row_diagnostics(args["plan"], 2)
-    assert all(route >= 100 for route, _ in routes), routes
+    assert all(route == 3 for route, _ in routes), routes
 
 
 # ---- Stream rows: temperature only and min-p, drawn slice by slice. ----
