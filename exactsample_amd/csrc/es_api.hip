@@ -97,12 +97,15 @@ int32_t es_launch(const es_arguments* args, void* stream_ptr) {
   const size_t need = es_workspace_size(a.rows, a.vocab, a.dispatch == 1);
   if (need == 0 || a.workspace_bytes < need) return ES_ERR_WORKSPACE_SIZE;
   if (reinterpret_cast<uintptr_t>(a.workspace) % 8 != 0) return ES_ERR_WORKSPACE_ALIGN;
-  if (a.dispatch == 1) return ES_ERR_BAD_OPTION;  // the on-device reference path is not built yet
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  // dispatch 1 ("reference"): every row is finished on the exact full-row
+  // path, so the slices gather no list candidates.
+  es_arguments run = a;
+  if (a.dispatch == 1) run.list_max = 0;
   const int64_t groups = (a.vocab + 3) / 4;
   const bool large_tiles = (a.target.dtype == ES_F32 || a.target.dtype == ES_BF16) &&
                            vectorizable_matrix(a, a.target) && vectorizable_matrix(a, a.draft);
-  const Geometry geo = choose_geometry(a.rows, groups, large_tiles, a.list_max);
+  const Geometry geo = choose_geometry(a.rows, groups, large_tiles, run.list_max);
   es::Plan pl{};
   pl.groups = int(groups);
   pl.req_blocks = int((a.requests + kBlock - 1) / kBlock);
@@ -118,10 +121,10 @@ int32_t es_launch(const es_arguments* args, void* stream_ptr) {
   hipError_t err = hipSuccess;
   if (geo.slices > es::MAX_SLICES) return ES_ERR_BAD_DIMENSION;  // vocabularies above ~1M are not supported yet
   switch (a.target.dtype) {
-    case ES_F32: err = es::launch_dtype<ES_F32>(a, pl, geo.g, vectorizable<ES_F32>(a), stream, g_split_event); break;
-    case ES_F64: err = es::launch_dtype<ES_F64>(a, pl, geo.g, vectorizable<ES_F64>(a), stream, g_split_event); break;
-    case ES_F16: err = es::launch_dtype<ES_F16>(a, pl, geo.g, vectorizable<ES_F16>(a), stream, g_split_event); break;
-    default: err = es::launch_dtype<ES_BF16>(a, pl, geo.g, vectorizable<ES_BF16>(a), stream, g_split_event); break;
+    case ES_F32: err = es::launch_dtype<ES_F32>(run, pl, geo.g, vectorizable<ES_F32>(a), stream, g_split_event); break;
+    case ES_F64: err = es::launch_dtype<ES_F64>(run, pl, geo.g, vectorizable<ES_F64>(a), stream, g_split_event); break;
+    case ES_F16: err = es::launch_dtype<ES_F16>(run, pl, geo.g, vectorizable<ES_F16>(a), stream, g_split_event); break;
+    default: err = es::launch_dtype<ES_BF16>(run, pl, geo.g, vectorizable<ES_BF16>(a), stream, g_split_event); break;
   }
   if (err != hipSuccess) {
     es::note_hip_error(err);

@@ -191,6 +191,11 @@ __device__ __forceinline__ int64_t request_of(const es_arguments& a, int64_t row
   return lo;
 }
 
+// The path_used value of every request of the call: dispatch 1 ("reference")
+// finishes every row on the exact full-row path (reference: verify.cu:5,51).
+__device__ __forceinline__ int32_t path_of(const es_arguments& a) {
+  return a.dispatch == 1 ? ES_PATH_REFERENCE : ES_PATH_FUSED;
+}
 __device__ __forceinline__ void write_failed_request(const es_arguments& a, int64_t req, int32_t status, int32_t path) {
   int64_t* tokens = a.tokens + req * a.token_s0;
   for (int64_t i = 0; i <= a.max_draft; ++i) tokens[i * a.token_s1] = -1;
@@ -548,7 +553,7 @@ __device__ __forceinline__ void finalize_request(const es_arguments& a, int64_t 
         if (lane == 0) {
           a.accepted[req * a.accepted_s] = 0;
           a.status[req * a.status_s] = first;
-          a.path[req * a.path_s] = ES_PATH_FUSED;
+          a.path[req * a.path_s] = path_of(a);
         }
         return;
       }
@@ -585,7 +590,7 @@ __device__ __forceinline__ void finalize_request(const es_arguments& a, int64_t 
   if (lane == 0) {
     a.accepted[req * a.accepted_s] = empty ? 0 : int32_t(accepted);
     a.status[req * a.status_s] = empty ? ES_INVALID_INPUT : ES_OK;
-    a.path[req * a.path_s] = ES_PATH_FUSED;
+    a.path[req * a.path_s] = path_of(a);
   }
 }
 
@@ -619,7 +624,7 @@ __device__ __forceinline__ void complete_row(const es_arguments& a, int64_t row,
     if (threadIdx.x == 0) {
       a.accepted[p.req * a.accepted_s] = 0;
       a.status[p.req * a.status_s] = result.status;
-      a.path[p.req * a.path_s] = ES_PATH_FUSED;
+      a.path[p.req * a.path_s] = path_of(a);
     }
   } else if (arrive(&counters(a, p.begin)->request, uint32_t(nrows), &sh.flag)) {
     if (wave_id() == 0) finalize_request(a, p.req);
@@ -2070,7 +2075,7 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4)))
     const int64_t req = int64_t(blockIdx.x) * BLOCK + tid;
     if (req < a.requests) {
       const int32_t st = metadata_status(a, req, malformed);
-      if (st != ES_OK) write_failed_request(a, req, st, ES_PATH_FUSED);
+      if (st != ES_OK) write_failed_request(a, req, st, path_of(a));
     }
     return;
   }
@@ -2382,7 +2387,7 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4)))
       perr = block_all(double(e), [](double x, double y) { return x + y; }, sh.dred, 0.0);
       pruned = block_all(pr, [](int x, int y) { return x + y; }, sh.ired, 0);
     }
-  } else if (stream_row(p, a.vocab) && !bad && valid > 0) {
+  } else if (a.dispatch != 1 && stream_row(p, a.vocab) && !bad && valid > 0) {
     const SliceDraw sd = slice_draw<DT, VEC>(a, row, slice, p, view, g0, g1, double(smax), first_id, pl.cap_slice, sh);
     psum = sd.sum;
     perr = sd.err;
@@ -2521,7 +2526,7 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments a, Plan pl) {
   const int list_max = a.list_max;
   const ListPlan lp = list_plan(p, list_max, pl.cap_slice, a.vocab);
   const bool sorted_list = lp.sorted_list, need_topp = lp.need_topp;
-  const bool stream = stream_row(p, a.vocab);
+  const bool stream = a.dispatch != 1 && stream_row(p, a.vocab);  // dispatch 1: the full-row path
   const bool stream_sum = stream && stream_sub(p) == 2u;  // the ratio test needs the kept mass
   if (wave_id() == 0) {
     if (lane < pl.slices) sh.n_cand[lane] = q.n_cand;

@@ -27,23 +27,40 @@ def _device(hip_device):
 DTYPES = ["float16", "bfloat16", "float32", "float64"]
 
 
+@pytest.mark.parametrize("dispatch", ["reference", "fused"])
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("k", [0, 1, 20, 35])
-def test_dtypes_strides_and_top_k(dtype, k):
+def test_dtypes_strides_and_top_k(dtype, k, dispatch):
+    """Forced paths as the reference's test_cuda.py:44-55 runs them; the
+    "reference" dispatch reports path_used 0 (every row on the exact full-row
+    path), "fused" 1."""
     import torch
     rows = np.random.default_rng(42).normal(size=(6, 35))
     run_and_compare(rows, [0, 1, 3, 6], [[-1, -1], [2, -1], [3, 4]], params=RequestParams(top_k=k),
-                    dtype=getattr(torch, dtype), strided=True)
+                    dtype=getattr(torch, dtype), strided=True, dispatch=dispatch)
 
 
+@pytest.mark.parametrize("dispatch", ["reference", "fused"])
 @pytest.mark.parametrize("list_max", [256, 0])
-def test_boundaries_and_packed_masks(list_max):
+def test_boundaries_and_packed_masks(list_max, dispatch):
     for p in [.5, np.nextafter(.5, 1), 1.]:
         run_and_compare(np.zeros((4, 4)), [0, 4], [[0, 1, 2]], params=RequestParams(top_k=4, top_p=p),
-                        list_max=list_max)
+                        list_max=list_max, dispatch=dispatch)
     mask = np.array([[-2147483648, 1]] * 3, np.int32)
     run_and_compare(np.zeros((3, 35)), [0, 3], [[31, 32]], mask=mask, params=RequestParams(top_k=20),
-                    strided=True, list_max=list_max)
+                    strided=True, list_max=list_max, dispatch=dispatch)
+
+
+def test_reference_dispatch_on_benchmark_rows():
+    """dispatch="reference" on 16 rows of the 128-request configuration
+    (V = 151,936): the full-row path for every row, path_used 0."""
+    import torch
+    import bench
+    work = bench.config2(seed=9, requests=16)
+    keys = work["keys"]
+    run_and_compare(work["rows"], work["offsets"], work["ids"], params=RequestParams(**work["params"]),
+                    rng=RngKey([int(x) for x in keys["seed"]], [int(x) for x in keys["stream"]], keys["positions"]),
+                    dtype=torch.float32, dispatch="reference")
 
 
 def test_statuses_and_atomicity():
