@@ -1,12 +1,14 @@
 """Benchmark of exactsample_amd's verify on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--cells 128x1,64x5] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--cells 128x1,64x5,...] [--no-cpu]
 
 A "step" is one ``verify`` call over one batch of synthetic logits already
 resident in HBM. The headline workload (value) is 128 requests x 1 row of
 V = 151,936 fp32 logits at T=0.6, top-k 20, top-p 0.95; the second cell is 64
 requests x (4 one-hot drafts + bonus) verified in ratio mode with the same
-settings. Rows come from the peaked generator: base N(mu, sigma^2) with
+settings. By default the same two batches are also timed as bfloat16 logits
+(the dtype of the reference's own benchmark); `--cells` adds 128 x 1 at
+T = 1.0 and at T = 0.7 top-p 0.9. Rows come from the peaked generator: base N(mu, sigma^2) with
 mu ~ U(-5, 0), sigma ~ U(2, 4); one token + U(6, 14); 15 tokens + U(0, 8);
 every even row rounded to the bf16 grid (values stay fp32).
 
@@ -170,7 +172,29 @@ def config5(seed=5, requests=256, variant="full_ratio"):
                 draft_logits=None if variant == "one_hot_coupled" else q)
 
 
-CELLS = {"128x1": config2, "64x5": config4}
+def as_bf16(work):
+    """The same rows handed over as bfloat16 (the reference's own benchmark dtype)."""
+    work["rows"] = round_to_bf16(work["rows"])
+    work["dtype"] = "bfloat16"
+    return work
+
+
+def with_params(work, **params):
+    work["params"] = dict(QWEN, **params)
+    return work
+
+
+# The value is the first cell; the others are reported beside it. The bf16
+# and other-settings cells follow the reference's own benchmark table
+# (128 x 1 and 64 x 5 at the Qwen settings, T = 1.0, and T = 0.7 top-p 0.9).
+CELLS = {
+    "128x1": config2,
+    "64x5": config4,
+    "128x1_bf16": lambda: as_bf16(config2()),
+    "64x5_bf16": lambda: as_bf16(config4()),
+    "128x1_T1": lambda: with_params(config2(), temperature=1.0, top_k=0, top_p=1.0),
+    "128x1_T0.7_p0.9": lambda: with_params(config2(), temperature=0.7, top_k=0, top_p=0.9),
+}
 
 
 def packed_mask(allowed):
@@ -202,7 +226,7 @@ def device_args(work, device="cuda"):
     rng = CudaRngKey(torch.as_tensor(work["keys"]["seed"], device=device),
                      torch.as_tensor(work["keys"]["stream"], device=device),
                      torch.as_tensor(work["keys"]["positions"], device=device))
-    logits = torch.as_tensor(work["rows"], device=device)
+    logits = torch.as_tensor(work["rows"], device=device).to(getattr(torch, work.get("dtype", "float32")))
     w = plan(logits.shape[0], requests, work["ids"].shape[1], logits.shape[1])
     args = dict(target_logits=logits, cu_rows=torch.as_tensor(work["offsets"], device=device),
                 draft_ids=torch.as_tensor(work["ids"], device=device), params=params, rng=rng, plan=w,
@@ -217,11 +241,12 @@ def device_args(work, device="cuda"):
 def algorithmic_bytes(work):
     """One read of every logit row plus parameters and outputs."""
     rows, vocab = work["rows"].shape
+    elem = 2 if work.get("dtype") == "bfloat16" else 4
     requests = len(work["offsets"]) - 1
     k1 = work["ids"].shape[1] + 1
     params = requests * (5 * 8 + 2 * 8) + rows * 8 + (requests + 1) * 8 + work["ids"].size * 8
     outputs = requests * (k1 * 8 + 3 * 4)
-    return rows * vocab * 4 + params + outputs
+    return rows * vocab * elem + params + outputs
 
 
 class Events:
@@ -457,7 +482,8 @@ def main():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=20)
-    parser.add_argument("--cells", default="128x1,64x5")
+    parser.add_argument("--cells", default="128x1,64x5,128x1_bf16,64x5_bf16",
+                        help=f"comma-separated cells of {', '.join(CELLS)}")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

@@ -503,7 +503,7 @@ __device__ __forceinline__ ListPlan list_plan(const Params& p, int list_max, int
     else lp.need = -1;
   }
   lp.L = lp.need > 0 ? min(lp.need, cap) : 0;
-  lp.sorted_list = lp.need > 0 && lp.L == lp.need && lp.need <= WAVE;
+  lp.sorted_list = lp.need > 0 && lp.L == lp.need && lp.need <= WAVE && p.top_k >= 1 && p.top_k <= list_max;
   lp.need_topp = lp.need == TOPP_SLICE_NEED && p.top_p < 1 && !(p.top_k >= 1 && p.top_k <= list_max);
   return lp;
 }
@@ -900,11 +900,12 @@ __device__ __forceinline__ bool list_finish(const es_arguments& a, int64_t row, 
     first_lo = block_all(first_lo, mn, sh.ired, INT_MAX);
     first_hi = block_all(first_hi, mn, sh.ired, INT_MAX);
     unsure = block_all(unsure, mn, sh.ired, INT_MAX);
-    if (unsure <= first_hi || first_lo != first_hi) { *why = 5; return false; }
-    if (first_hi == INT_MAX) {
-      if (!whole) { *why = 6; return false; }  // the nucleus may extend past the list
+    if (first_lo == INT_MAX && first_hi == INT_MAX && unsure == INT_MAX) {
+      // No prefix of the list reaches the target.
+      if (!whole) { *why = 6; return false; }  // the nucleus extends past the list
       n2 = n1;
     } else {
+      if (unsure <= first_hi || first_lo != first_hi) { *why = 5; return false; }
       n2 = first_hi + 1;
     }
   }
@@ -1834,7 +1835,9 @@ __device__ __forceinline__ SliceDraw slice_draw(const es_arguments& a, int64_t r
     KahanSum ks;
     pk = range_pick<B, true>(a, row, view, g0, g1, ts, p.rng, sub, excluded, floor_of(), maybe_kept, &ks);
     out.sum = block_all(double(ks.s) - double(ks.c), [](double x, double y) { return x + y; }, sh.dred, 0.0);
-    out.err = block_all(double(ks.e), [](double x, double y) { return x + y; }, sh.dred, 0.0);
+    // The FP32 terms' bound, the Kahan sums' and the block's FP64 tree.
+    out.err = 1.01 * block_all(double(ks.e), [](double x, double y) { return x + y; }, sh.dred, 0.0) +
+              4.8e-7 * out.sum;
     out.pruned = block_all(ks.pruned, [](int x, int y) { return x + y; }, sh.ired, 0);
     pk = block_pick(pk, sh);
   } else {
@@ -2364,27 +2367,42 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4)))
       frontier = INFINITY;  // nothing certain
       fid = -1;
     }
-    // Top-p lists also need the kept weights' sum, relative to the slice maximum.
+    // Top-p lists also need the kept weights' sum, relative to the slice
+    // maximum, in FP64: each weight exp((l - max) / T) within 5e-15 of its
+    // value (|x| <= 40 for the terms summed), Kahan sums per thread and a
+    // block tree; 1e-14 S bounds the error. Weights below e^-40 are counted,
+    // not summed.
     if (need_topp) {
-      const double ms = double(smax);
-      const float inv_t = float(1.0 / p.temperature);
-      const bool slow = !(inv_t < 1e30f);
-      float s = 0, c = 0, e = 0;
+      const double ms = double(smax), T = p.temperature;
+      double s = 0, c = 0;
       int pr = 0;
-      mem([&](int, int, W x, int) {
-        float xl;
-        if constexpr (sizeof(W) == 8) xl = float((double(x) - ms) / p.temperature);
-        else xl = slow ? float(double(x - float(ms)) / p.temperature) : (x - float(ms)) * inv_t;
-        const bool ok = x > neg_inf<W>();
-        const bool counted = ok && xl >= SUM_PRUNE;
-        pr += ok && !counted;
-        const float w = expf(counted ? xl : -100.f) * (counted ? 1.f : 0.f);
-        const float d = w - c, t2 = s + d;
-        c = (t2 - s) - d; s = t2;
-        e += w * (X_ERR * (1.f + fabsf(counted ? xl : 0.f)));
-      });
-      psum = block_all(double(s) - double(c), [](double x, double y) { return x + y; }, sh.dred, 0.0);
-      perr = block_all(double(e), [](double x, double y) { return x + y; }, sh.dred, 0.0);
+      for (int base = g0 + tid; base < g1; base += 4 * BLOCK) {
+        W x[4][4];
+        uint32_t mb[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int g = base + u * BLOCK;
+          view.load(min(g, g1 - 1), x[u]);
+          mb[u] = g < g1 ? group_bits(a, row, g) : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const bool ok = ((mb[u] >> j) & 1u) && x[u][j] > neg_inf<W>();
+            const double xl = (double(x[u][j]) - ms) / T;
+            const bool counted = ok && xl >= double(SUM_PRUNE);
+            pr += ok && !counted;
+            if (counted) {
+              const double d = exp(xl) - c, t2 = s + d;
+              c = (t2 - s) - d;
+              s = t2;
+            }
+          }
+        }
+      }
+      psum = block_all(s - c, [](double x, double y) { return x + y; }, sh.dred, 0.0);
+      perr = 1e-14 * psum;
       pruned = block_all(pr, [](int x, int y) { return x + y; }, sh.ired, 0);
     }
   } else if (a.dispatch != 1 && stream_row(p, a.vocab) && !bad && valid > 0) {
@@ -2559,7 +2577,7 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments a, Plan pl) {
         const double shift = (t2.v1 - q.max_v) / p.temperature;
         const double scale = exp(-shift);
         if (shift > 700) { s_err = (q.sum + q.err) * scale + q.pruned * SUM_PRUNE_W; s_pr = 0; }
-        else { s_sum = q.sum * scale; s_err = (1.01 * q.err + 4.8e-7 * q.sum) * scale * (1 + 1e-14); }
+        else { s_sum = q.sum * scale; s_err = (q.err + 4e-16 * q.sum) * scale * (1 + 1e-14); }
       }
       s_sum = wave_all(s_sum, [](double x, double y) { return x + y; }, 0.0);
       s_err = wave_all(s_err, [](double x, double y) { return x + y; }, 0.0);

@@ -64,8 +64,8 @@ struct SlicePart {
   double second_v;   // second in (value desc, id asc) order, -inf
   double frontier;   // largest valid logit not stored as a candidate; -inf if none, +inf if unusable
   double tau;        // a stream row's reference maximum: its pick's scores are relative to it
-  double sum;        // FP32 sum of exp((l - max_v) / T) over kept tokens, for top-p lists
-  double err;        // its error bound
+  double sum;        // sum of exp((l - max_v) / T) over kept tokens: FP64 for top-p lists, FP32 for ratio stream rows
+  double err;        // a bound on its error (tokens below e^-40 excluded: they are `pruned`)
   int32_t max_id, second_id, valid, n_cand, pruned, flags;
 };
 static_assert(sizeof(SlicePart) == 72, "SlicePart layout");
