@@ -972,7 +972,8 @@ struct SlotMap {
 template <class W>
 __device__ __forceinline__ int wave_topk(const es_arguments& a, int64_t row, const Params& p, Shared<W>& sh,
                                          const Cand<W> (&pre)[WAVE_BATCH], const SlotMap& map, int slices, int cap,
-                                         double M, double F, int F_id, int valid_all, RowResult* out) {
+                                         int lane_n_cand, double M, double F, int F_id, int valid_all,
+                                         RowResult* out) {
   using K = typename std::conditional<sizeof(W) == 8, uint64_t, uint32_t>::type;
   const int lane = lane_id();
   const int pref = map.pref;
@@ -991,15 +992,22 @@ __device__ __forceinline__ int wave_topk(const es_arguments& a, int64_t row, con
     const double d = double(c.v);
     return d > F || (d == F && c.id <= F_id);
   };
+  // The slot's slice count is read for every slot first (independent LDS
+  // reads, one wait), then the slots are appended.
+  bool take_r[WAVE_BATCH];
 #pragma unroll
   for (int r = 0; r < WAVE_BATCH; ++r) {
     const int idx = lane + WAVE * r;
     const int sl = map.slice(idx);
-    add(idx < slices * pref && idx - sl * pref < sh.n_cand[min(sl, MAX_SLICES - 1)] && at_or_before_F(pre[r]), pre[r]);
+    const int n_sl = sh.n_cand[min(sl, MAX_SLICES - 1)];
+    take_r[r] = (idx < slices * pref) & (idx - sl * pref < n_sl);
   }
+#pragma unroll
+  for (int r = 0; r < WAVE_BATCH; ++r) add(take_r[r] && at_or_before_F(pre[r]), pre[r]);
   // Candidates beyond the prefetch (a slice that stored more than `pref`).
   const Cand<W>* cands = candidates<W>(a, row);
-  for (int sl = 0; sl < slices; ++sl) {
+  const bool overflow = __ballot(lane < slices && lane_n_cand > pref) != 0;
+  for (int sl = 0; overflow && sl < slices; ++sl) {
     const int n_s = sh.n_cand[sl];
     for (int base = pref; base < n_s; base += WAVE) {
       const int i = base + lane;
@@ -2061,10 +2069,30 @@ __device__ __forceinline__ void slice_cut(const Visit& visit, int L, W floor, Sh
 
 // ---------------------------------------------------------------------------
 // The kernel.
+// The kernels' arguments read in place, in the kernel argument segment. A
+// by-value kernel parameter whose address is taken (every helper takes the
+// arguments by reference) is first copied whole into registers at kernel
+// entry: 98 dwords that do not fit in SGPRs, so the copy runs as a chain of
+// load, wait and spill rounds before any of the kernel's own loads. Read in
+// place, each field is a scalar load where it is used. The explicit
+// arguments sit at the segment's start in declaration order, each at its
+// natural alignment, which is also KernelArgs' layout.
+struct KernelArgs {
+  es_arguments a;
+  Plan pl;
+};
+static_assert(offsetof(KernelArgs, pl) == sizeof(es_arguments), "Plan follows es_arguments");
+__device__ __forceinline__ const KernelArgs& kernel_args() {
+  typedef const __attribute__((address_space(4))) KernelArgs* ArgPtr;
+  return *(const KernelArgs*)(ArgPtr)__builtin_amdgcn_kernarg_segment_ptr();
+}
+
 template <int DT, bool VEC, int G>
-__global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4))) es_main(es_arguments a, Plan pl) {
+__global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(5))) es_main(es_arguments, Plan) {
   using W = typename Ty<DT>::W;
   __shared__ Shared<W> sh;
+  const es_arguments& a = kernel_args().a;
+  const Plan pl = kernel_args().pl;
   const int tid = threadIdx.x;
   const int lane = lane_id();
 
@@ -2206,13 +2234,17 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4)))
     int bad_l = 0, valid_l = 0;
     W m2 = neg_inf<W>();
     fid_l = INT_MAX;
+    // A fresh copy of gb: the tile's load addresses are then not reused here,
+    // so the compiler need not keep all of them alive across the stats pass.
+    int gbx = gb;
+    asm volatile("" : "+v"(gbx));
     // Four groups in flight at a time (the scheduling barrier keeps the
     // compiler from hoisting every load, which would hold a second tile).
 #pragma unroll
     for (int i0 = 0; i0 < G; i0 += 4) {
       W x[4][4];
 #pragma unroll
-      for (int q = 0; q < 4 && i0 + q < G; ++q) view.load(min(gb + BLOCK * (i0 + q), g1 - 1), x[q]);
+      for (int q = 0; q < 4 && i0 + q < G; ++q) view.load(min(gbx + BLOCK * (i0 + q), g1 - 1), x[q]);
 #pragma unroll
       for (int q = 0; q < 4 && i0 + q < G; ++q) {
         const int i = i0 + q;
@@ -2510,9 +2542,11 @@ __device__ __forceinline__ bool stream_finish(const es_arguments& a, int64_t row
 // (reference: fused.cuh:803-933 prologue, :1250-1412 list, :1446-1810 full
 // row). The row is then committed (verify.cu:169-217 for drafted requests).
 template <int DT, bool VEC>
-__global__ void __launch_bounds__(BLOCK) es_finish(es_arguments a, Plan pl) {
+__global__ void __launch_bounds__(BLOCK) es_finish(es_arguments, Plan) {
   using W = typename Ty<DT>::W;
   __shared__ Shared<W> sh;
+  const es_arguments& a = kernel_args().a;
+  const Plan pl = kernel_args().pl;
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -2628,7 +2662,8 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments a, Plan pl) {
     RowResult wr{0, 1, -1, -1, ES_OK, ES_OK};
     if (sorted_list && bsum == 0 && vsum > 0) {
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      wdone = wave_topk(a, row, p, sh, pre, map, pl.slices, pl.cap_slice, t2.v1, fr.v, fr.id, vsum, &wr);
+      wdone = wave_topk(a, row, p, sh, pre, map, pl.slices, pl.cap_slice, q.n_cand, t2.v1, fr.v, fr.id, vsum,
+                        &wr);
     }
     if (lane == 0) {
       sh.wdone = wdone;
