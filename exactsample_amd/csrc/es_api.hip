@@ -118,6 +118,7 @@ int32_t es_launch(const es_arguments* args, void* stream_ptr) {
   }
   const int cap_total = a.target.dtype == ES_F64 ? es::cand_capacity<double>() : es::cand_capacity<float>();
   pl.cap_slice = cap_total / pl.slices;
+  pl.slice_blocks = int(a.rows * pl.slices);
   hipError_t err = hipSuccess;
   if (geo.slices > es::MAX_SLICES) return ES_ERR_BAD_DIMENSION;  // vocabularies above ~1M are not supported yet
   switch (a.target.dtype) {

@@ -2087,6 +2087,24 @@ __device__ __forceinline__ const KernelArgs& kernel_args() {
   return *(const KernelArgs*)(ArgPtr)__builtin_amdgcn_kernarg_segment_ptr();
 }
 
+// A request block (reference: verify.cu:6-56 initialize), run by es_finish:
+// the offsets check, header word 0, and the outputs of requests whose
+// metadata is invalid. Header word 1 (the FP64 recompute count) is cleared by
+// es_main's first block, or here when there are no rows.
+__device__ __forceinline__ void request_block(const es_arguments& a, int rb) {
+  const int tid = threadIdx.x;
+  const bool malformed = offsets_malformed(a);
+  if (rb == 0 && tid == 0) {
+    reinterpret_cast<int32_t*>(a.workspace)[0] = malformed;
+    if (a.rows == 0) reinterpret_cast<uint32_t*>(a.workspace)[1] = 0;
+  }
+  const int64_t req = int64_t(rb) * BLOCK + tid;
+  if (req < a.requests) {
+    const int32_t st = metadata_status(a, req, malformed);
+    if (st != ES_OK) write_failed_request(a, req, st, path_of(a));
+  }
+}
+
 template <int DT, bool VEC, int G>
 __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(5))) es_main(es_arguments, Plan) {
   using W = typename Ty<DT>::W;
@@ -2096,23 +2114,12 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(5)))
   const int tid = threadIdx.x;
   const int lane = lane_id();
 
-  // ---- Request blocks. ----
-  if (int(blockIdx.x) < pl.req_blocks) {
-    const bool malformed = offsets_malformed(a);
-    if (blockIdx.x == 0 && tid == 0) {
-      reinterpret_cast<int32_t*>(a.workspace)[0] = malformed;
-      reinterpret_cast<uint32_t*>(a.workspace)[1] = 0;
-    }
-    const int64_t req = int64_t(blockIdx.x) * BLOCK + tid;
-    if (req < a.requests) {
-      const int32_t st = metadata_status(a, req, malformed);
-      if (st != ES_OK) write_failed_request(a, req, st, path_of(a));
-    }
-    return;
-  }
+  // Every block is a slice block: the request checks run in the finishing
+  // kernel, so that none of this kernel's resident slots is held by them.
+  if (blockIdx.x == 0 && tid == 0) reinterpret_cast<uint32_t*>(a.workspace)[1] = 0;  // the FP64 recompute count
 
   // ---- Slice blocks. ----
-  const int b = int(blockIdx.x) - pl.req_blocks;
+  const int b = int(blockIdx.x);
   const int64_t row = b / pl.slices;
   const int slice = b - int(row) * pl.slices;
   const int vocab = int(a.vocab);
@@ -2547,6 +2554,10 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments, Plan) {
   __shared__ Shared<W> sh;
   const es_arguments& a = kernel_args().a;
   const Plan pl = kernel_args().pl;
+  if (int64_t(blockIdx.x) >= a.rows) {
+    request_block(a, int(int64_t(blockIdx.x) - a.rows));
+    return;
+  }
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -2741,13 +2752,16 @@ hipError_t launch_main(const es_arguments& a, const Plan& pl, hipStream_t stream
   es_arguments args = a;
   Plan plan = pl;
   void* params[] = {&args, &plan};
-  const unsigned blocks = unsigned(pl.req_blocks + a.rows * pl.slices);
-  hipError_t err = hipLaunchKernel(reinterpret_cast<const void*>(&es_main<DT, VEC, G>), dim3(blocks), dim3(BLOCK),
-                                   params, 0, stream);
+  // es_main: the slice blocks; es_finish: one block per row, then the
+  // request blocks.
+  hipError_t err = hipSuccess;
+  if (a.rows > 0)
+    err = hipLaunchKernel(reinterpret_cast<const void*>(&es_main<DT, VEC, G>), dim3(unsigned(pl.slice_blocks)),
+                          dim3(BLOCK), params, 0, stream);
   if (err == hipSuccess && split) err = hipEventRecord(split, stream);
-  if (err != hipSuccess || a.rows == 0) return err;
-  return hipLaunchKernel(reinterpret_cast<const void*>(&es_finish<DT, VEC>), dim3(unsigned(a.rows)), dim3(BLOCK),
-                         params, 0, stream);
+  if (err != hipSuccess) return err;
+  return hipLaunchKernel(reinterpret_cast<const void*>(&es_finish<DT, VEC>),
+                         dim3(unsigned(a.rows + pl.req_blocks)), dim3(BLOCK), params, 0, stream);
 }
 
 // Contiguous rows aligned to a group of four use vector loads and, for f32

@@ -14,9 +14,9 @@ struct Plan {
   int32_t slices;        // blocks per row
   int32_t groups;        // groups of 4 tokens per row
   int32_t gps;           // groups per slice
-  int32_t req_blocks;    // request blocks at the front of the grid
+  int32_t req_blocks;    // request blocks, after the row blocks of es_finish
   int32_t cap_slice;     // candidates one slice may store
-  int32_t pad;
+  int32_t slice_blocks;  // rows x slices: es_main's grid
 };
 
 // Launches the two kernels of a call for logits of dtype DT with a register
