@@ -955,7 +955,23 @@ constexpr int UNION_PER_LANE = 8;  // union entries per lane the wave selects fr
 // readlane (no LDS round trips).
 template <class W> __device__ __forceinline__ int wave_rank(W v, int id, int n) {
   int rank = 0;
-  for (int j = 0; j < n; ++j) rank += before(lane_read(v, j), lane_read(id, j), v, id);
+  if constexpr (sizeof(W) == 4) {
+    // One 64-bit key per entry, larger = earlier: the value's order key, then
+    // the inverted ID. Read four lanes at a time, so the reads of a batch do
+    // not wait on one another.
+    const uint64_t key = (uint64_t(order_key(v)) << 32) | uint64_t(~uint32_t(id));
+    int j = 0;
+    for (; j + 4 <= n; j += 4) {
+      uint64_t k[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) k[u] = lane_read(key, j + u);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) rank += k[u] > key;
+    }
+    for (; j < n; ++j) rank += lane_read(key, j) > key;
+  } else {
+    for (int j = 0; j < n; ++j) rank += before(lane_read(v, j), lane_read(id, j), v, id);
+  }
   return rank;
 }
 
@@ -1021,58 +1037,65 @@ __device__ __forceinline__ int wave_topk(const es_arguments& a, int64_t row, con
   const int n_keep = p.top_k > 0 && p.top_k < valid_all ? int(p.top_k) : valid_all;
   if (n_u > WAVE * UNION_PER_LANE) return 0;
   if (n_u < n_keep || n_keep < 1) return -1;  // cannot happen for a complete union
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  // Bins of the union by distance below the row maximum (quarter logits, the
-  // last bin for 63.75 and more): monotone in the order, so the bins up to the
-  // one holding the n_keep-th entry hold a prefix of the order (the pool).
-  unsigned* bins = reinterpret_cast<unsigned*>(sh.u.list.sid);  // HEAD_BINS counters
-#pragma unroll
-  for (int r = 0; r < HEAD_BINS / WAVE; ++r) bins[lane + WAVE * r] = 0;
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  const int per = (n_u + WAVE - 1) / WAVE;
-  int bin_of[UNION_PER_LANE];
-#pragma unroll
-  for (int r = 0; r < UNION_PER_LANE; ++r) {
-    const int idx = lane + WAVE * r;
-    bin_of[r] = HEAD_BINS;
-    if (r < per && idx < n_u) {
-      bin_of[r] = head_bin(M - double(sh.u.list.v[idx]));
-      atomicAdd(&bins[bin_of[r]], 1u);
-    }
-  }
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  // Lane l owns bins [4l, 4l + 4): the first bin whose running total reaches n_keep.
-  constexpr int BPL = HEAD_BINS / WAVE;
-  unsigned bc[BPL], local = 0;
-#pragma unroll
-  for (int q = 0; q < BPL; ++q) { bc[q] = bins[BPL * lane + q]; local += bc[q]; }
-  const unsigned incl_b = wave_scan_add(local);
-  int mine_cut = INT_MAX;
-  unsigned run = incl_b - local;
-#pragma unroll
-  for (int q = 0; q < BPL; ++q) {
-    run += bc[q];
-    if (mine_cut == INT_MAX && run >= unsigned(n_keep)) mine_cut = BPL * lane + q;
-  }
-  const int cut_bin = wave_all(mine_cut, [](int x, int y) { return x < y ? x : y; }, INT_MAX);
-  // The pool: union entries in bins up to cut_bin, one per lane.
-  int n_pool = 0;
-#pragma unroll
-  for (int r = 0; r < UNION_PER_LANE; ++r) {
-    if (r >= per) break;
-    const int idx = lane + WAVE * r;
-    const bool take = idx < n_u && bin_of[r] <= cut_bin;
-    const uint64_t mk = __ballot(take);
-    const int pos = n_pool + __popcll(mk & ((1ull << lane) - 1ull));
-    if (take && pos < WAVE) { sh.u.list.sv[pos] = sh.u.list.v[idx]; sh.u.list.w[pos] = double(sh.u.list.id[idx]); }
-    n_pool += __popcll(mk);
-  }
-  if (n_pool > WAVE) return 0;  // a wide tie at the k-th value
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  // Rank sort of the pool, one entry per lane.
   W v = neg_inf<W>();
   int id = INT_MAX;
-  if (lane < n_pool) { v = sh.u.list.sv[lane]; id = int(sh.u.list.w[lane]); }
+  int n_pool;
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  if (n_u <= WAVE) {
+    // The whole union fits one entry per lane: it is the pool.
+    n_pool = n_u;
+    if (lane < n_pool) { v = sh.u.list.v[lane]; id = sh.u.list.id[lane]; }
+  } else {
+    // Bins of the union by distance below the row maximum (quarter logits, the
+    // last bin for 63.75 and more): monotone in the order, so the bins up to the
+    // one holding the n_keep-th entry hold a prefix of the order (the pool).
+    unsigned* bins = reinterpret_cast<unsigned*>(sh.u.list.sid);  // HEAD_BINS counters
+#pragma unroll
+    for (int r = 0; r < HEAD_BINS / WAVE; ++r) bins[lane + WAVE * r] = 0;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const int per = (n_u + WAVE - 1) / WAVE;
+    int bin_of[UNION_PER_LANE];
+#pragma unroll
+    for (int r = 0; r < UNION_PER_LANE; ++r) {
+      const int idx = lane + WAVE * r;
+      bin_of[r] = HEAD_BINS;
+      if (r < per && idx < n_u) {
+        bin_of[r] = head_bin(M - double(sh.u.list.v[idx]));
+        atomicAdd(&bins[bin_of[r]], 1u);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    // Lane l owns bins [4l, 4l + 4): the first bin whose running total reaches n_keep.
+    constexpr int BPL = HEAD_BINS / WAVE;
+    unsigned bc[BPL], local = 0;
+#pragma unroll
+    for (int q = 0; q < BPL; ++q) { bc[q] = bins[BPL * lane + q]; local += bc[q]; }
+    const unsigned incl_b = wave_scan_add(local);
+    int mine_cut = INT_MAX;
+    unsigned run = incl_b - local;
+#pragma unroll
+    for (int q = 0; q < BPL; ++q) {
+      run += bc[q];
+      if (mine_cut == INT_MAX && run >= unsigned(n_keep)) mine_cut = BPL * lane + q;
+    }
+    const int cut_bin = wave_all(mine_cut, [](int x, int y) { return x < y ? x : y; }, INT_MAX);
+    // The pool: union entries in bins up to cut_bin, one per lane.
+    n_pool = 0;
+#pragma unroll
+    for (int r = 0; r < UNION_PER_LANE; ++r) {
+      if (r >= per) break;
+      const int idx = lane + WAVE * r;
+      const bool take = idx < n_u && bin_of[r] <= cut_bin;
+      const uint64_t mk = __ballot(take);
+      const int pos = n_pool + __popcll(mk & ((1ull << lane) - 1ull));
+      if (take && pos < WAVE) { sh.u.list.sv[pos] = sh.u.list.v[idx]; sh.u.list.w[pos] = double(sh.u.list.id[idx]); }
+      n_pool += __popcll(mk);
+    }
+    if (n_pool > WAVE) return 0;  // a wide tie at the k-th value
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    // Rank sort of the pool, one entry per lane.
+    if (lane < n_pool) { v = sh.u.list.sv[lane]; id = int(sh.u.list.w[lane]); }
+  }
   const int rank = wave_rank(v, id, n_pool);
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   if (lane < n_pool) { sh.u.list.v[rank] = v; sh.u.list.id[rank] = id; }
