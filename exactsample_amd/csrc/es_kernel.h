@@ -2584,12 +2584,12 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments, Plan) {
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = lane_id();
-  // One round of loads: the row's parameters (recorded by its first slice
-  // block), the slices' summaries and every candidate slot wave 0 may need.
-  const Params p = *row_meta(a, row);
+  // One round of loads: the slices' summaries and every candidate slot wave 0
+  // may need, then the row's parameters (recorded by its first slice block).
+  // The summaries and slots are issued first: they depend on nothing loaded,
+  // and issued after the parameters they would wait for them.
   const SlotMap map(min(pl.cap_slice, WAVE * WAVE_BATCH / pl.slices));
   Cand<W> pre[WAVE_BATCH];
-  if (tid == 0) counters(a, row)->max_key = 0;  // the slices published their maxima; ready for the next call
   SlicePart q;
   q.max_v = -INFINITY; q.second_v = -INFINITY; q.frontier = -INFINITY; q.tau = -INFINITY;
   q.sum = 0; q.err = 0; q.max_id = INT_MAX; q.second_id = INT_MAX; q.valid = 0; q.n_cand = 0; q.pruned = 0; q.flags = 0;
@@ -2604,6 +2604,8 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments, Plan) {
       if (idx < pl.slices * map.pref) pre[r] = cands[sl * pl.cap_slice + (idx - sl * map.pref)];
     }
   }
+  const Params p = *row_meta(a, row);
+  if (tid == 0) counters(a, row)->max_key = 0;  // the slices published their maxima; ready for the next call
   if (p.status != ES_OK || p.meta_bad) {
     // Malformed offsets or invalid request metadata: the request block reports it.
     skip_row(a, row);
