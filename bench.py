@@ -7,8 +7,9 @@ resident in HBM. The headline workload (value) is 128 requests x 1 row of
 V = 151,936 fp32 logits at T=0.6, top-k 20, top-p 0.95; the second cell is 64
 requests x (4 one-hot drafts + bonus) verified in ratio mode with the same
 settings. By default the same two batches are also timed as bfloat16 logits
-(the dtype of the reference's own benchmark); `--cells` adds 128 x 1 at
-T = 1.0 and at T = 0.7 top-p 0.9. Rows come from the peaked generator: base N(mu, sigma^2) with
+(the dtype of the reference's own benchmark), and both shapes are timed at the
+reference benchmark's other two settings, T = 1.0 and T = 0.7 top-p 0.9.
+Rows come from the peaked generator: base N(mu, sigma^2) with
 mu ~ U(-5, 0), sigma ~ U(2, 4); one token + U(6, 14); 15 tokens + U(0, 8);
 every even row rounded to the bf16 grid (values stay fp32).
 
@@ -193,7 +194,9 @@ CELLS = {
     "128x1_bf16": lambda: as_bf16(config2()),
     "64x5_bf16": lambda: as_bf16(config4()),
     "128x1_T1": lambda: with_params(config2(), temperature=1.0, top_k=0, top_p=1.0),
+    "64x5_T1": lambda: with_params(config4(), temperature=1.0, top_k=0, top_p=1.0),
     "128x1_T0.7_p0.9": lambda: with_params(config2(), temperature=0.7, top_k=0, top_p=0.9),
+    "64x5_T0.7_p0.9": lambda: with_params(config4(), temperature=0.7, top_k=0, top_p=0.9),
 }
 
 
@@ -482,7 +485,8 @@ def main():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=20)
-    parser.add_argument("--cells", default="128x1,64x5,128x1_bf16,64x5_bf16",
+    parser.add_argument("--cells", default="128x1,64x5,128x1_bf16,64x5_bf16,128x1_T1,64x5_T1,128x1_T0.7_p0.9,"
+                                           "64x5_T0.7_p0.9",
                         help=f"comma-separated cells of {', '.join(CELLS)}")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = parser.parse_args()
