@@ -1327,28 +1327,47 @@ template <int DT, bool VEC> struct FullRow {
   }
 
   // The first composite key (descending order) among tokens where pred holds at
-  // which the correctly rounded running sum of weight(t, v) reaches target.
-  template <class Pred, class Wt> __device__ __forceinline__ u128 mass_boundary(double target, Pred&& pred, Wt&& weight) {
+  // which the correctly rounded running sum of weight(t, v) reaches top_p
+  // times the correctly rounded sum of all of them (reference.py:73-83). The
+  // first histogram pass, which reads every weight, also sums them: a
+  // certified double-double sum, or the exact sum when its rounding is not
+  // certain.
+  template <class Pred, class Wt>
+  __device__ __forceinline__ u128 mass_boundary(double top_p, Pred&& pred, Wt&& weight) {
     constexpr int NB = CK<W>::BITS;
     constexpr int D = 11;
     u128 prefix = 0;
     int known = 0;
     double base_lo = 0, base_hi = 0;  // exact mass before the current region
-    const double below_t = nextafter(target, 0.0);
+    double target = 0, below_t = 0;
     while (known < NB) {
       const int width = min(D, NB - known), shift = NB - known - width;
       const int buckets = 1 << width;
       for (int i = threadIdx.x; i < buckets; i += BLOCK) { sh.u.hist.cnt[i] = 0; sh.u.hist.mass[i] = 0; }
       __syncthreads();
+      DD acc{0, 0};
+      int n_all = 0;
       each<false>([&](int t, W v, bool ok) {
         if (!pred(t, v, ok)) return;
         const u128 ck = CK<W>::make(v, t);
         if (known && (ck >> (NB - known)) != prefix) return;
         const int d = int(ck >> shift) & (buckets - 1);
+        const double w = weight(t, v);
         atomicAdd(&sh.u.hist.cnt[d], 1u);
-        atomicAdd(&sh.u.hist.mass[d], weight(t, v));
+        atomicAdd(&sh.u.hist.mass[d], w);
+        if (!known && w > 0) { acc = dd_add(acc, DD{w, 0}); ++n_all; }
       });
       __syncthreads();
+      if (!known) {
+        acc = block_dd(acc, sh);
+        n_all = block_all(n_all, [](int x, int y) { return x + y; }, sh.ired, 0);
+        double total;
+        if (!dd_round_certain(acc, dd_sum_error(acc, n_all), &total))
+          total = exact_sum<false>([&](int t, W v, bool ok) -> double { return pred(t, v, ok) ? weight(t, v) : 0.0; },
+                                   false);
+        target = top_p * total;
+        below_t = nextafter(target, 0.0);
+      }
       const int per = (buckets + BLOCK - 1) / BLOCK;
       // Walk buckets in descending order with interval bounds.
       double local = 0, local_err = 0;
@@ -1588,27 +1607,30 @@ template <int DT, bool VEC> struct FullRow {
     tp.init(maximum, p.temperature, p.min_p);
     // ---- Kept set: valid, min-p and positivity (a prefix of the order). ----
     auto kept = [&](int, W v, bool ok) { return valid_tok(v, ok) && tp.kept(v, tp.x32(v)); };
-    int nk = 0;
-    each<false>([&](int t, W v, bool ok) { nk += kept(t, v, ok); });
-    nk = block_all(nk, [](int x, int y) { return x + y; }, sh.ired, 0);
     // ---- Top-k: an exact cut at the k-th token (reference.py:67-71). ----
+    // The kept count is needed only when k may cut: k < valid tokens.
     u128 cut = 0;  // keep ck >= cut
-    if (p.top_k > 0 && p.top_k < nk) cut = select_nth(int(p.top_k), kept);
+    if (p.top_k > 0 && p.top_k < valid) {
+      int nk = 0;
+      each<false>([&](int t, W v, bool ok) { nk += kept(t, v, ok); });
+      nk = block_all(nk, [](int x, int y) { return x + y; }, sh.ired, 0);
+      if (p.top_k < nk) cut = select_nth(int(p.top_k), kept);
+    }
     auto in_k = [&](int t, W v, bool ok) { return kept(t, v, ok) && CK<W>::make(v, t) >= cut; };
     auto w64 = [&](int, W v) -> double { return exp(tp.x64(v)); };
     double den = 0;
     bool den_exact = false;
     // ---- Top-p: the shortest prefix whose fsum reaches top_p * fsum(all) (reference.py:73-85). ----
     if (p.top_p < 1) {
-      const double total = exact_sum<false>([&](int t, W v, bool ok) -> double {
-        return in_k(t, v, ok) ? w64(t, v) : 0.0;
-      }, false);
-      const double target = p.top_p * total;
-      cut = mass_boundary(target, in_k, w64);
-      den = exact_sum<false>([&](int t, W v, bool ok) -> double {
-        return in_k(t, v, ok) && CK<W>::make(v, t) >= cut ? w64(t, v) : 0.0;
-      }, false);
-      den_exact = true;
+      cut = mass_boundary(p.top_p, in_k, w64);
+      // The kept mass is needed by the ratio test and the residual only: a
+      // draw compares x + G, the same for every token up to log(den).
+      if (p.verify) {
+        den = exact_sum<false>([&](int t, W v, bool ok) -> double {
+          return in_k(t, v, ok) && CK<W>::make(v, t) >= cut ? w64(t, v) : 0.0;
+        }, false);
+        den_exact = true;
+      }
     }
     auto in_final = [&](int t, W v, bool ok) { return in_k(t, v, ok) && CK<W>::make(v, t) >= cut; };
     // The floor of a draw: the first token of the order that the draw may take.
