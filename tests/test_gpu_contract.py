@@ -175,6 +175,27 @@ def test_real_vocabulary_shape(k):
     run_and_compare(rows, [0, 2], [[123]], params=RequestParams(top_k=k), dtype=torch.bfloat16)
 
 
+def test_requests_without_rows_are_invalid():
+    # No rows at all: only the request checks run (reference: verify.cu:6-56,
+    # a segment of 1..max_draft+1 rows). The recompute count is cleared too.
+    import torch
+    from exactsample_amd.cuda import CudaRequestParams, CudaRngKey, plan, verify
+    work = plan(4, 4, 1, 8)
+    work.workspace.fill_(0xff)  # stale header words from an earlier call
+    out = work.allocate_output()
+    one64 = torch.zeros(1, dtype=torch.int64, device="cuda")
+    onef = torch.ones(1, dtype=torch.float64, device="cuda")
+    verify(torch.zeros((0, 8), device="cuda"), torch.zeros(2, dtype=torch.int64, device="cuda"),
+           torch.zeros((1, 1), dtype=torch.int64, device="cuda"),
+           params=CudaRequestParams(onef, one64, onef, torch.zeros(1, dtype=torch.float64, device="cuda"), one64 * 0),
+           rng=CudaRngKey(one64, one64, torch.zeros(0, dtype=torch.int64, device="cuda")), plan=work, out=out)
+    assert work.fallbacks() == 0
+    assert out.num_requests == 1
+    assert out.status[:1].cpu().tolist() == [int(Status.INVALID_INPUT)]
+    assert out.tokens[:1].cpu().tolist() == [[-1, -1]]
+    assert out.accepted_len[:1].cpu().tolist() == [0]
+
+
 def test_empty_batch_is_valid():
     import torch
     from exactsample_amd.cuda import CudaRequestParams, CudaRngKey, plan, verify
