@@ -1123,9 +1123,7 @@ __device__ __forceinline__ int wave_topk(const es_arguments& a, int64_t row, con
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     if (lane < n) sacc_add(sh.limbs, wk);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    r = 0;
-    if (lane == 0) r = sacc_round(sh.limbs);
-    return lane_read(r, 0);
+    return sacc_round_wave(sh.limbs);
   };
   if (n1 == 0) return -1;  // the maximum always survives; defensive
   double den = rounded_prefix(n1);

@@ -80,4 +80,45 @@ __device__ __forceinline__ double sacc_round(unsigned long long* limbs) {
   return ldexp(double(mant), lowbit + drop - 1074);
 }
 
+// The same correctly rounded sum, computed by one whole wave (every lane calls
+// it and gets the result) without touching the limbs: lane i holds limb i,
+// carries move up one lane per step until none is left (at most one per limb
+// after the first step), and the leading limb, the significand bits and the
+// sticky flag are read across lanes.
+__device__ __forceinline__ double sacc_round_wave(const unsigned long long* limbs) {
+  const int lane = int(__lane_id());
+  unsigned long long v = lane < SACC_LIMBS ? limbs[lane] : 0ull;
+  while (__ballot((v >> 32) != 0)) {
+    const unsigned long long up = __shfl_up(v >> 32, 1u);
+    v = (v & 0xffffffffull) + (lane > 0 ? up : 0ull);
+    if (lane >= SACC_LIMBS) v = 0;  // beyond the top limb: out of contract, dropped as the serial loop does
+  }
+  const unsigned long long nz = __ballot(v != 0);
+  if (!nz) return 0.0;
+  auto limb = [&](int i) -> uint64_t { return i < SACC_LIMBS ? uint64_t(__shfl(v, i)) : 0; };
+  const int top = 63 - __clzll((long long)nz);
+  const int lead = 31 - __clz(uint32_t(limb(top)));
+  const int nbits = top * 32 + lead + 1;
+  if (nbits <= 53) {
+    const uint64_t x = (limb(1) << 32) | limb(0);
+    return ldexp(double(x), -1074);
+  }
+  const int lowbit = nbits - 64 > 0 ? nbits - 64 : 0;
+  const int li = lowbit >> 5, sh = lowbit & 31;
+  const uint64_t w0 = limb(li), w1 = limb(li + 1), w2 = limb(li + 2);
+  const uint64_t lo64 = w0 | (w1 << 32);
+  const uint64_t w = sh ? (lo64 >> sh) | (w2 << (64 - sh)) : lo64;
+  bool sticky = __ballot(lane < li && v != 0) != 0;  // any set bit below lowbit
+  if (sh && (w0 & ((1ull << sh) - 1))) sticky = true;
+  const int width = nbits - lowbit;
+  const int drop = width - 53;
+  uint64_t mant = w >> drop;
+  const uint64_t rest = w & ((uint64_t(1) << drop) - 1), half = uint64_t(1) << (drop - 1);
+  if (rest > half || (rest == half && (sticky || (mant & 1)))) {
+    ++mant;
+    if (mant == (uint64_t(1) << 53)) return ldexp(double(mant >> 1), lowbit + drop + 1 - 1074);
+  }
+  return ldexp(double(mant), lowbit + drop - 1074);
+}
+
 }  // namespace es
