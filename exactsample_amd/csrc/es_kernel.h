@@ -743,7 +743,10 @@ template <class W> __device__ __forceinline__ double list_fsum(Shared<W>& sh, in
   __syncthreads();
   for (int i = threadIdx.x; i < n; i += BLOCK) sacc_add(sh.limbs, sh.u.list.w[i]);
   __syncthreads();
-  if (threadIdx.x == 0) sh.dred[0] = sacc_round(sh.limbs);
+  if (wave_id() == 0) {  // rounded across wave 0, read by the block
+    const double sum = sacc_round_wave(sh.limbs);
+    if (lane_id() == 0) sh.dred[0] = sum;
+  }
   __syncthreads();
   r = sh.dred[0];
   __syncthreads();
@@ -1260,7 +1263,10 @@ template <int DT, bool VEC> struct FullRow {
       if (w > 0) sacc_add(sh.limbs, w);
     });
     __syncthreads();
-    if (threadIdx.x == 0) { sh.dred[0] = sacc_round(sh.limbs); }
+    if (wave_id() == 0) {  // rounded across wave 0, read by the block
+      const double sum = sacc_round_wave(sh.limbs);
+      if (lane_id() == 0) sh.dred[0] = sum;
+    }
     __syncthreads();
     r = sh.dred[0];
     __syncthreads();

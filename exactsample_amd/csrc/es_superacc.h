@@ -1,6 +1,6 @@
 // Exact sums of non-negative doubles in LDS: every term is split into 32-bit
 // chunks of its exact value in units of 2^-1074 and added to 64-bit limbs with
-// LDS atomics; one thread then propagates carries and rounds to nearest, ties
+// LDS atomics; one wave then propagates carries and rounds to nearest, ties
 // to even. The result equals Python's math.fsum (the correctly rounded exact
 // sum) of the same terms, in any order. Used only when a double-double sum
 // cannot certify its own rounding.
@@ -36,52 +36,9 @@ __device__ __forceinline__ void sacc_add(unsigned long long* limbs, double w) {
   if (c2) atomicAdd(&limbs[limb + 2], (unsigned long long)c2);
 }
 
-// Run by one thread after the adds are visible: the correctly rounded sum.
-// Propagates carries in place (the limbs then hold 32-bit digits), then reads
-// the top 64 bits and a sticky flag word by word.
-__device__ __forceinline__ double sacc_round(unsigned long long* limbs) {
-  unsigned long long carry = 0;
-  int top = -1;
-  for (int i = 0; i < SACC_LIMBS; ++i) {
-    const unsigned long long t = limbs[i] + carry;
-    limbs[i] = t & 0xffffffffull;
-    carry = t >> 32;
-    if (limbs[i]) top = i;
-  }
-  if (top < 0) return 0.0;
-  // The number is sum(limbs[i] << 32 i) units of 2^-1074. Take bits
-  // [lowbit, lowbit + 64) into a 64-bit word w with its leading bit set.
-  const int lead = 31 - __clz(uint32_t(limbs[top]));
-  const int nbits = top * 32 + lead + 1;
-  if (nbits <= 53) {
-    const uint64_t x = (uint64_t(top >= 1 ? limbs[1] : 0) << 32) | limbs[0];
-    return ldexp(double(x), -1074);
-  }
-  const int lowbit = nbits - 64 > 0 ? nbits - 64 : 0;
-  auto bits_from = [&](int b) -> uint64_t {  // 64 bits starting at bit b
-    const int li = b >> 5, sh = b & 31;
-    const uint64_t w0 = li < SACC_LIMBS ? limbs[li] : 0, w1 = li + 1 < SACC_LIMBS ? limbs[li + 1] : 0,
-                   w2 = li + 2 < SACC_LIMBS ? limbs[li + 2] : 0;
-    const uint64_t lo64 = w0 | (w1 << 32);
-    return sh ? (lo64 >> sh) | (w2 << (64 - sh)) : lo64;
-  };
-  uint64_t w = bits_from(lowbit);
-  bool sticky = false;  // any set bit below lowbit
-  for (int i = 0; i < (lowbit >> 5) && !sticky; ++i) sticky = limbs[i] != 0;
-  if ((lowbit & 31) && (limbs[lowbit >> 5] & ((1ull << (lowbit & 31)) - 1))) sticky = true;
-  const int width = nbits - lowbit;   // bits held in w (<= 64), leading bit at width - 1
-  const int drop = width - 53;        // bits of w below the significand
-  uint64_t mant = w >> drop;
-  const uint64_t rest = w & ((uint64_t(1) << drop) - 1), half = uint64_t(1) << (drop - 1);
-  if (rest > half || (rest == half && (sticky || (mant & 1)))) {
-    ++mant;
-    if (mant == (uint64_t(1) << 53)) return ldexp(double(mant >> 1), lowbit + drop + 1 - 1074);
-  }
-  return ldexp(double(mant), lowbit + drop - 1074);
-}
-
-// The same correctly rounded sum, computed by one whole wave (every lane calls
-// it and gets the result) without touching the limbs: lane i holds limb i,
+// The correctly rounded sum, computed by one whole wave once the adds are
+// visible (every lane calls it and gets the result), without touching the
+// limbs: lane i holds limb i,
 // carries move up one lane per step until none is left (at most one per limb
 // after the first step), and the leading limb, the significand bits and the
 // sticky flag are read across lanes.
@@ -91,7 +48,7 @@ __device__ __forceinline__ double sacc_round_wave(const unsigned long long* limb
   while (__ballot((v >> 32) != 0)) {
     const unsigned long long up = __shfl_up(v >> 32, 1u);
     v = (v & 0xffffffffull) + (lane > 0 ? up : 0ull);
-    if (lane >= SACC_LIMBS) v = 0;  // beyond the top limb: out of contract, dropped as the serial loop does
+    if (lane >= SACC_LIMBS) v = 0;  // beyond the top limb: out of contract, dropped
   }
   const unsigned long long nz = __ballot(v != 0);
   if (!nz) return 0.0;
