@@ -1817,7 +1817,12 @@ __device__ __forceinline__ Pick range_pick(const es_arguments& a, int64_t row, c
   using W = typename Ty<DT>::W;
   Pick best = pick_none();
   float bar = floor - PRUNE_MARGIN;
-  for (int base = g_begin + int(threadIdx.x); base < g_end; base += B * BLOCK) {
+  // Every lane runs the same number of rounds (groups past the range carry no
+  // tokens), so after each round the wave can share its best lower bound: a
+  // token whose upper bound stays below it cannot win, and is kept only as a
+  // loser's bound, as with the thread's own best.
+  for (int base0 = g_begin; base0 < g_end; base0 += B * BLOCK) {
+    const int base = base0 + int(threadIdx.x);
     W x[B][4];
     uint32_t mb[B];
 #pragma unroll
@@ -1828,6 +1833,8 @@ __device__ __forceinline__ Pick range_pick(const es_arguments& a, int64_t row, c
     }
 #pragma unroll
     for (int u = 0; u < B; ++u) pick_group<SUM>(base + u * BLOCK, x[u], mb[u], tp, rng, sub, excluded, keep, best, bar, sum);
+    const float wave_lo = wave_all(best.lo, [](float p, float q) { return p > q ? p : q; }, -INFINITY);
+    bar = fmaxf(bar, wave_lo - PRUNE_MARGIN);
   }
   return best;
 }
