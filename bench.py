@@ -1,4 +1,4 @@
-"""Benchmark of exactsample_amd's verify on one MI355X.
+"""Benchmark of exactsample's verify (the gfx950 build) on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--cells 128x1,64x5,...] [--no-cpu]
 
@@ -211,7 +211,7 @@ def packed_mask(allowed):
 
 def device_args(work, device="cuda"):
     import torch
-    from exactsample_amd.cuda import CudaRequestParams, CudaRngKey, plan
+    from exactsample.cuda import CudaRequestParams, CudaRngKey, plan
 
     requests = len(work["offsets"]) - 1
     p = work["params"]
@@ -326,7 +326,7 @@ def time_cell(name, steps, warmup):
 
     Every timed call is queued behind a spin kernel, so calls run back to back.
     - value: the C ABI (es_launch) with an event before and after each call;
-    - op: the same through exactsample_amd.cuda.verify (the torch op; it also
+    - op: the same through exactsample.cuda.verify (the torch op; it also
       records the plan's completion event each call, which costs GPU time);
     - split: es_launch with a third event recorded by the library between the
       slice-stream kernel (es_main) and the per-row finishing kernel
@@ -336,8 +336,8 @@ def time_cell(name, steps, warmup):
       Infinity Cache.
     """
     import torch
-    from exactsample_amd import capi
-    from exactsample_amd.cuda import verify
+    from exactsample import capi
+    from exactsample.cuda import verify
 
     work = CELLS[name]()
     args = device_args(work)
@@ -498,7 +498,7 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 2
-    from exactsample_amd.cuda import load_library
+    from exactsample.cuda import load_library
     load_library()
     copy = copy_rate(VOCAB * 4 * 128)
     print(json.dumps({"copy": copy}), file=sys.stderr, flush=True)

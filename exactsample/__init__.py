@@ -1,8 +1,8 @@
-"""exactsample_amd: exact token sampling and speculative-draft verification on MI355X.
+"""exactsample: exact token sampling and speculative-draft verification on MI355X (gfx950).
 
 A from-scratch gfx950 implementation of exactsample's device path behind the
-same API: ``plan`` and ``verify`` (exactsample_amd.cuda), the data model
-(exactsample_amd.types) and the ``torch.ops.exactsample.verify_out`` op, a thin
+same API: ``plan`` and ``verify`` (exactsample.cuda), the data model
+(exactsample.types) and the ``torch.ops.exactsample.verify_out`` op, a thin
 binding over the C ABI in include/exactsample_amd.h.
 
 The FP64 CPU oracle of the reference (``verify_reference`` and friends) is not

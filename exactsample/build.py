@@ -1,7 +1,7 @@
 """Builds the gfx950 library and the PyTorch op binding in place.
 
-    python -m exactsample_amd.build            # both
-    python -m exactsample_amd.build --lib-only # the C-ABI library only
+    python -m exactsample.build            # both
+    python -m exactsample.build --lib-only # the C-ABI library only
 
 Outputs (next to this file):
   libexactsample_amd.so       HIP kernels + the C ABI of include/exactsample_amd.h

@@ -1,6 +1,7 @@
 // Host side of exactsample_amd: launch geometry, dtype dispatch and the C ABI
 // (include/exactsample_amd.h).
 #include <limits.h>
+#include <atomic>
 #include <stdio.h>
 #include "es_layout.h"
 #include "es_plan.h"
@@ -9,6 +10,15 @@ namespace {
 constexpr int kBlock = 256;  // threads per block of the kernel
 thread_local char g_last_hip_error[256] = "";
 thread_local hipEvent_t g_split_event = nullptr;
+std::atomic<uint32_t> g_generation{0};
+
+// A tag for the row maxima a call publishes in its workspace: consecutive
+// calls get different tags, and 0 (a zeroed word) is never one.
+uint32_t next_generation() {
+  uint32_t g = g_generation.fetch_add(1, std::memory_order_relaxed) + 1;
+  if (g == 0) g = g_generation.fetch_add(1, std::memory_order_relaxed) + 1;
+  return g;
+}
 
 constexpr int64_t elem_size(int dt) { return dt == ES_F64 ? 8 : dt == ES_F32 ? 4 : 2; }
 
@@ -109,18 +119,29 @@ int32_t es_launch(const es_arguments* args, void* stream_ptr) {
   es::Plan pl{};
   pl.groups = int(groups);
   pl.req_blocks = int((a.requests + kBlock - 1) / kBlock);
-  if (geo.slices > es::MAX_SLICES || a.rows == 0) {
+  // A vocabulary needing more than MAX_SLICES tiles gives each slice several
+  // tiles (read group by group) and stores no list candidates.
+  int64_t tiles = 1, slices = geo.slices;
+  if (slices > es::MAX_SLICES) {
+    tiles = (slices + es::MAX_SLICES - 1) / es::MAX_SLICES;
+    const int64_t span = tiles * geo.g * kBlock;
+    slices = (groups + span - 1) / span;
+    run.list_max = 0;
+  }
+  if (a.rows == 0) {
     pl.slices = 1;
     pl.gps = int(groups);
+    pl.tiles = 1;
   } else {
-    pl.slices = geo.slices;
-    pl.gps = geo.g * kBlock;  // every slice but the last is exactly one tile
+    pl.slices = int(slices);
+    pl.gps = int(tiles * geo.g * kBlock);  // every slice but the last is exactly `tiles` tiles
+    pl.tiles = int(tiles);
   }
   const int cap_total = a.target.dtype == ES_F64 ? es::cand_capacity<double>() : es::cand_capacity<float>();
   pl.cap_slice = cap_total / pl.slices;
   pl.slice_blocks = int(a.rows * pl.slices);
+  pl.generation = next_generation();
   hipError_t err = hipSuccess;
-  if (geo.slices > es::MAX_SLICES) return ES_ERR_BAD_DIMENSION;  // vocabularies above ~1M are not supported yet
   switch (a.target.dtype) {
     case ES_F32: err = es::launch_dtype<ES_F32>(run, pl, geo.g, vectorizable<ES_F32>(a), stream, g_split_event); break;
     case ES_F64: err = es::launch_dtype<ES_F64>(run, pl, geo.g, vectorizable<ES_F64>(a), stream, g_split_event); break;

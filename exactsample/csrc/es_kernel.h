@@ -2,22 +2,23 @@
 //
 // Two kernels per call (es_launch), on the caller's stream:
 //
-//  es_main, a grid of 256-thread blocks of two kinds:
-//  * request blocks (the first ceil(R / 256)): validate each request's
-//    metadata and write the outputs of every request that fails it; they also
-//    clear the call's header words (reference: csrc/verify/verify.cu:6-56,
-//    initialize);
-//  * slice blocks (rows x slices, one register tile of up to 16 x 4 logits per
-//    thread): one pass over a slice of a row: validation (NaN/+inf anywhere),
-//    the valid count, the two largest valid logits and, for rows a list can
-//    finish, every valid logit at or above a threshold chosen so that the
-//    slice's top L are stored, or exactly its first L after a radix cut
-//    (reference: fused.cuh:409-519 row_stats, :686-798 row_hist/row_gather).
-//    Each slice writes a SlicePart with plain stores; the row's first slice
-//    also records the row's resolved request parameters.
+//  es_main, rows x slices blocks of 256 threads, each one register tile of up
+//  to 16 x 4 logits per thread (several tiles, read group by group, when the
+//  vocabulary needs more than MAX_SLICES tiles): one pass over a slice of a
+//  row: validation (NaN/+inf anywhere), the valid count, the largest valid
+//  logit and, for rows a list can finish, every valid logit at or above a
+//  threshold chosen so that the slice's top L are stored, or exactly its first
+//  L after a radix cut (reference: fused.cuh:409-519 row_stats, :686-798
+//  row_hist/row_gather); stream rows also draw their slice's certified
+//  Gumbel-max (reference: fused.cuh:532-681 row_scan). Each slice writes a
+//  SlicePart with plain stores; the row's first slice also records the row's
+//  resolved request parameters and checks its per-row metadata.
 //
-//  es_finish, one block per row (the kernel boundary makes every slice's
-//  stores visible): merges the slices in slice order and finishes the row:
+//  es_finish, one block per row, then ceil(R / 256) request blocks that
+//  validate each request's metadata and write the outputs of every request
+//  that fails it (reference: csrc/verify/verify.cu:6-56, initialize). A row
+//  block (the kernel boundary makes every slice's stores visible) merges the
+//  slices in slice order and finishes the row:
 //    - failed and greedy rows directly;
 //    - top-k rows from the union of the slices' candidates in one wave, in FP64
 //      with the oracle's formulas (reference: fused.cuh:1250-1412);
@@ -241,19 +242,44 @@ template <class T> __device__ __forceinline__ T fetch(const T* src) {
 // Every thread's outstanding stores acknowledged (s_waitcnt vmcnt(0)).
 __device__ __forceinline__ void stores_done() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// Arrival on a counter; true in every thread of the block that arrives last,
-// which also resets the counter and may then fetch what the others published.
+// Arrival on a counter (zeroed earlier in the call); true in every thread of
+// the block that arrives last, which may then fetch what the others
+// published. The arrival is an agent-scope acquire-release operation: every
+// block's stores (acknowledged by every wave, then the barrier) happen before
+// its arrival, and the last block's later loads happen after all arrivals.
 __device__ __forceinline__ bool arrive(uint32_t* counter, uint32_t expected, int* s_flag) {
   stores_done();
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t old = atomicAdd(counter, 1u);
-    const int last = old + 1 == expected;
-    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_flag = last;
+    const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = old + 1 == expected;
   }
   __syncthreads();
   return *s_flag != 0;
+}
+
+// The largest slice maximum of a row published in this call: the word holds
+// (generation << 32) | key; one of another generation (an earlier call, a
+// fresh workspace) counts as nothing published. Keys only grow within a call,
+// and each row has at most MAX_SLICES publishers, so the loop ends.
+__device__ __forceinline__ void publish_max(unsigned long long* word, uint32_t gen, uint32_t key) {
+  const unsigned long long mine = (static_cast<unsigned long long>(gen) << 32) | key;
+  unsigned long long old = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  while (uint32_t(old >> 32) != gen || uint32_t(old) < key) {
+    const unsigned long long seen = atomicCAS(word, old, mine);
+    if (seen == old) break;
+    old = seen;
+  }
+}
+// The published maximum (a lower bound on the row maximum), -inf if none.
+__device__ __forceinline__ double published_max(unsigned long long* word, uint32_t gen) {
+  const unsigned long long v = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return uint32_t(v >> 32) == gen ? double(key_value(uint32_t(v))) : -INFINITY;
+}
+// The largest float at or below v.
+__device__ __forceinline__ float float_at_or_below(double v) {
+  const float f = float(v);
+  return double(f) > v ? nextafterf(f, -INFINITY) : f;
 }
 
 // ---------------------------------------------------------------------------
@@ -595,8 +621,9 @@ __device__ __forceinline__ void finalize_request(const es_arguments& a, int64_t 
 }
 
 // The call's FP64 recomputation count, workspace word 1: cleared by es_main's
-// request blocks, then added to by each es_finish block that needed one (the
-// kernel boundary orders the two).
+// first block (or by the first request block of a call without rows), then
+// added to by each es_finish block that needed one (the kernel boundary
+// orders the two).
 __device__ __forceinline__ void add_fallbacks(const es_arguments& a, unsigned n) {
   if (n) atomicAdd(reinterpret_cast<unsigned*>(a.workspace) + 1, n);
 }
@@ -1854,7 +1881,7 @@ struct SliceDraw { double sum, err, mref; int pruned; };
 template <int DT, bool VEC, class W>
 __device__ __forceinline__ SliceDraw slice_draw(const es_arguments& a, int64_t row, int slice, Params p,
                                              const RowView<DT, VEC>& view, int g0, int g1, double smax, int first_id,
-                                             int cap_slice, Shared<W>& sh) {
+                                             int cap_slice, uint32_t gen, Shared<W>& sh) {
   constexpr int B = 4;  // groups in flight per thread
   const int tid = threadIdx.x;
   load_row_rng(a, row, &p);
@@ -1862,7 +1889,7 @@ __device__ __forceinline__ SliceDraw slice_draw(const es_arguments& a, int64_t r
   const int excluded = sub == 2u ? p.draft_id : -1;
   unsigned long long* key = &counters(a, row)->max_key;
   auto published = [&]() {
-    if (tid == 0) sh.dred[0] = key_value(uint64_t(__hip_atomic_load(key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
+    if (tid == 0) sh.dred[0] = published_max(key, gen);
     __syncthreads();
     const double m = sh.dred[0];
     __syncthreads();
@@ -1870,8 +1897,8 @@ __device__ __forceinline__ SliceDraw slice_draw(const es_arguments& a, int64_t r
   };
   double mref = smax;
   if (p.min_p > 0) {
-    if (tid == 0) atomicMax(key, (unsigned long long)order_key(smax));
-    mref = published();
+    if (tid == 0) publish_max(key, gen, order_key(float_at_or_below(smax)));
+    mref = fmax(smax, published());
   }
   Temp<W> ts;
   ts.init(mref, p.temperature, p.min_p);
@@ -2161,6 +2188,124 @@ __device__ __forceinline__ void request_block(const es_arguments& a, int rb) {
   }
 }
 
+// A slice block's request lookup and, in the row's first slice, the record
+// the finishing block reads: the request's parameters, its per-row metadata
+// check and the RNG address. The request's first row also zeroes the
+// request's arrival counter, which the finishing kernel counts on after the
+// kernel boundary.
+template <class W>
+__device__ __forceinline__ void slice_params(const es_arguments& a, int64_t row, int slice, int64_t x0, int64_t x1,
+                                             Params* p, Shared<W>& sh) {
+  slice_lookup(a, row, x0, x1, p, sh);
+  if (slice == 0 && wave_id() == 0) {
+    if (p->status == ES_OK) {
+      load_row_rng(a, row, p);
+      p->meta_bad = !request_rows_ok(a, *p);
+    }
+    if (lane_id() == 0) {
+      *row_meta(a, row) = *p;
+      if (p->status == ES_OK && row == p->begin) counters(a, row)->request = 0;
+    }
+  }
+}
+
+// The slice's summary, written by one thread with plain stores (the kernel
+// boundary makes it visible to the finishing kernel).
+__device__ __forceinline__ void write_part(const es_arguments& a, int64_t row, int slice, double smax, int first_id,
+                                           double frontier, int frontier_id, double tau, double sum, double err,
+                                           int valid, int n_cand, int pruned, int bad) {
+  SlicePart part;
+  part.max_v = smax;
+  part.second_v = -INFINITY;
+  part.frontier = frontier;
+  part.tau = tau;  // a stream row's reference maximum for its pick
+  part.sum = sum;
+  part.err = err;
+  part.max_id = first_id;
+  part.second_id = frontier_id;
+  part.valid = valid;
+  part.n_cand = n_cand;
+  part.pruned = pruned;
+  part.flags = bad;
+  slice_parts(a, row)[slice] = part;
+}
+
+// A slice of several register tiles (a vocabulary past MAX_SLICES tiles):
+// the statistics over the slice read group by group (NaN/+inf anywhere, the
+// valid count, the maximum with its lowest ID) and the streaming draw. Such
+// calls store no list candidates (the host runs them with list_max 0), so
+// filtered rows take the full-row path.
+template <int DT, bool VEC>
+__device__ __noinline__ void wide_slice(const es_arguments& a, const Plan& pl, int64_t row, int slice, int64_t x0,
+                                        int64_t x1, Shared<typename Ty<DT>::W>& sh) {
+  using W = typename Ty<DT>::W;
+  const int tid = threadIdx.x, lane = lane_id();
+  Params p;
+  slice_params(a, row, slice, x0, x1, &p, sh);
+  if (p.status != ES_OK) return;
+  const RowView<DT, VEC> view(a.target, row, int(a.vocab));
+  const int g0 = slice * pl.gps, g1 = min(g0 + pl.gps, pl.groups);
+  int bad_l = 0, valid_l = 0, fid_l = INT_MAX;
+  W m_l = neg_inf<W>();
+  for (int base = g0 + tid; base < g1; base += 4 * BLOCK) {
+    W x[4][4];
+    uint32_t mb[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int g = base + u * BLOCK;
+      view.load(min(g, g1 - 1), x[u]);
+      mb[u] = g < g1 ? group_bits(a, row, g) : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int g = base + u * BLOCK;
+      if (g >= g1) continue;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const W y = x[u][j];
+        bad_l |= y != y || y == W(INFINITY);
+        const bool ok = ((mb[u] >> j) & 1u) && y > neg_inf<W>();
+        valid_l += ok;
+        if (ok && y > m_l) { m_l = y; fid_l = 4 * g + j; }
+      }
+    }
+  }
+  struct MI { W v; int id; };
+  const MI wm = wave_all(MI{m_l, fid_l}, [](MI x, MI y) { return (y.v > x.v || (y.v == x.v && y.id < x.id)) ? y : x; },
+                         MI{neg_inf<W>(), INT_MAX});
+  const int valid_w = wave_all(valid_l, [](int x, int y) { return x + y; }, 0);
+  const int bad_w = __ballot(bad_l) != 0;
+  if (lane == 0) {
+    sh.st_max[wave_id()] = wm.v;
+    sh.st_id[wave_id()] = wm.id;
+    sh.st_valid[wave_id()] = valid_w;
+    sh.st_bad[wave_id()] = bad_w;
+  }
+  __syncthreads();
+  W smax = neg_inf<W>();
+  int first_id = INT_MAX, valid = 0, bad = 0;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) {
+    if (sh.st_max[w] > smax || (sh.st_max[w] == smax && sh.st_id[w] < first_id)) {
+      smax = sh.st_max[w];
+      first_id = sh.st_id[w];
+    }
+    valid += sh.st_valid[w];
+    bad |= sh.st_bad[w];
+  }
+  double psum = 0, perr = 0, tau = -INFINITY;
+  int pruned = 0;
+  if (a.dispatch != 1 && stream_row(p, a.vocab) && !bad && valid > 0) {
+    const SliceDraw sd = slice_draw<DT, VEC>(a, row, slice, p, view, g0, g1, double(smax), first_id, pl.cap_slice,
+                                             pl.generation, sh);
+    psum = sd.sum;
+    perr = sd.err;
+    pruned = sd.pruned;
+    tau = sd.mref;
+  }
+  if (tid == 0) write_part(a, row, slice, double(smax), first_id, -INFINITY, INT_MAX, tau, psum, perr, valid, 0, pruned, bad);
+}
+
 template <int DT, bool VEC, int G>
 __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(5))) es_main(es_arguments, Plan) {
   using W = typename Ty<DT>::W;
@@ -2191,6 +2336,10 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(5)))
     x0 = at(a.cu_rows, tid);
     x1 = at(a.cu_rows, tid + 1);
   }
+  if (pl.tiles > 1) {
+    wide_slice<DT, VEC>(a, pl, row, slice, x0, x1, sh);
+    return;
+  }
   __builtin_amdgcn_sched_barrier(0);
   // Tile loads. Groups past the slice's end are loaded as copies of its last
   // group: they never change the maximum or the checks below, and `allow`
@@ -2215,16 +2364,7 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(5)))
     allow &= mbits;
   }
   Params p;
-  slice_lookup(a, row, x0, x1, &p, sh);
-  if (slice == 0 && wave_id() == 0) {
-    // The row's first slice records what the finishing block needs: the
-    // request's parameters, its per-row metadata check and the RNG address.
-    if (p.status == ES_OK) {
-      load_row_rng(a, row, &p);
-      p.meta_bad = !request_rows_ok(a, p);
-    }
-    if (lane == 0) *row_meta(a, row) = p;
-  }
+  slice_params(a, row, slice, x0, x1, &p, sh);
   if (p.status != ES_OK) return;
   const ListPlan lp = list_plan(p, a.list_max, pl.cap_slice, a.vocab);
   int need = lp.need;
@@ -2501,28 +2641,14 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(5)))
       pruned = block_all(pr, [](int x, int y) { return x + y; }, sh.ired, 0);
     }
   } else if (a.dispatch != 1 && stream_row(p, a.vocab) && !bad && valid > 0) {
-    const SliceDraw sd = slice_draw<DT, VEC>(a, row, slice, p, view, g0, g1, double(smax), first_id, pl.cap_slice, sh);
+    const SliceDraw sd = slice_draw<DT, VEC>(a, row, slice, p, view, g0, g1, double(smax), first_id, pl.cap_slice,
+                                             pl.generation, sh);
     psum = sd.sum;
     perr = sd.err;
     pruned = sd.pruned;
     tau = sd.mref;
   }
-  if (tid == 0) {
-    SlicePart part;
-    part.max_v = double(smax);
-    part.second_v = -INFINITY;
-    part.frontier = frontier;
-    part.tau = tau;  // a stream row's reference maximum for its pick
-    part.sum = psum;
-    part.err = perr;
-    part.max_id = first_id;
-    part.second_id = fid;  // the frontier's ID
-    part.valid = valid;
-    part.n_cand = n_cand;
-    part.pruned = pruned;
-    part.flags = bad;
-    slice_parts(a, row)[slice] = part;
-  }
+  if (tid == 0) write_part(a, row, slice, double(smax), first_id, frontier, fid, tau, psum, perr, valid, n_cand, pruned, bad);
 }
 
 // ---------------------------------------------------------------------------
@@ -2598,9 +2724,10 @@ __device__ __forceinline__ bool stream_finish(const es_arguments& a, int64_t row
 
 // ---------------------------------------------------------------------------
 // The finishing kernel: one block per row, after the slice pass (the kernel
-// boundary makes the slices' summaries and candidates visible). Wave 1 checks
-// the request's per-row metadata while wave 0 merges the slices in slice order
-// and, for a top-k row, finishes it; then the block routes the row: failed,
+// boundary makes the slices' summaries and candidates visible). Wave 0 merges
+// the slices in slice order and, for a top-k row, finishes it (the row's
+// first slice block already checked the per-row metadata); then the block
+// routes the row: failed,
 // greedy, finished by the wave, the FP64 block list, or the full-row path
 // (reference: fused.cuh:803-933 prologue, :1250-1412 list, :1446-1810 full
 // row). The row is then committed (verify.cu:169-217 for drafted requests).

@@ -6,9 +6,11 @@
 //                     32 B RowResult + 12288 B scratch per row, api.h:37-43):
 //                     result, state, counters, meta, slice parts, candidates
 //
-// A row's region sits at a fixed address whatever the call's row count, so the
-// arrival counters inside it stay where the previous call left them (zero):
-// every counter is reset by the block that completes it.
+// No byte of the workspace has to hold a particular value when a call starts
+// (a fresh, poisoned or half-used workspace all work): every word a call
+// reads is written earlier in the same call, the arrival counters are reset
+// by the slice pass before the finishing kernel counts on them, and the
+// published row maxima carry the call's generation.
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
@@ -50,9 +52,11 @@ struct RowState {
 static_assert(sizeof(RowState) == 48, "RowState layout");
 
 // request: rows of the request completed (an arrival counter, kept in the
-// request's first row). max_key: the largest slice maximum published so far
-// in this call (an order key; 0 is below every value), which min-p slices
-// read as a lower bound on the row maximum. Both are back to 0 after a call.
+// request's first row; set to 0 by the slice pass of that row's first slice).
+// max_key: the largest slice maximum published so far in this call, as
+// (generation << 32) | FP32 order key of the maximum rounded down; min-p
+// slices read it as a lower bound on the row maximum, and a word of another
+// generation counts as nothing published.
 struct Counters {
   uint32_t request, pad;
   unsigned long long max_key;

@@ -17,6 +17,8 @@ struct Plan {
   int32_t req_blocks;    // request blocks, after the row blocks of es_finish
   int32_t cap_slice;     // candidates one slice may store
   int32_t slice_blocks;  // rows x slices: es_main's grid
+  int32_t tiles;         // register tiles per slice (> 1 only for vocabularies past MAX_SLICES tiles)
+  uint32_t generation;   // this call's tag for the published row maxima (never repeats on consecutive calls)
 };
 
 // Launches the two kernels of a call for logits of dtype DT with a register

@@ -55,8 +55,8 @@ def c_library():
     if _clib is None:
         path = _HERE / _LIB_NAME
         if not path.is_file():
-            raise RuntimeError(f"exactsample_amd library is missing: {path}. Build it with "
-                               "`python -m exactsample_amd.build`.")
+            raise RuntimeError(f"exactsample library (libexactsample_amd.so) is missing: {path}. Build it with "
+                               "`python -m exactsample.build`.")
         lib = ctypes.CDLL(str(path))
         lib.es_workspace_size.restype = ctypes.c_size_t
         lib.es_workspace_size.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32]
@@ -79,7 +79,7 @@ def load_library(path: str | os.PathLike[str] | None = None) -> None:
     library = Path(requested) if requested else _HERE / _OPS_NAME
     if not library.is_file():
         raise RuntimeError(f"exactsample op library is missing: {library}. Build it with "
-                           "`python -m exactsample_amd.build`, or set EXACTSAMPLE_LIBRARY.")
+                           "`python -m exactsample.build`, or set EXACTSAMPLE_LIBRARY.")
     torch.ops.load_library(str(library.resolve()))
 
 

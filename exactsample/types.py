@@ -1,4 +1,4 @@
-"""Public data model of exactsample_amd.
+"""Public data model of exactsample (the MI355X build).
 
 Mirrors python/exactsample/types.py:7-44 of the reference (Status, PathUsed,
 RequestParams, RngKey, VerifyOutput) so callers switching packages keep their

@@ -3,7 +3,7 @@
  * Drop-in boundary for the reference's C++ API (include/exactsample/api.h:7-44)
  * and the op binding that fills it (csrc/bindings.cpp:45-136). Plain C types,
  * plain pointers and sizes; no PyTorch types. A thin PyTorch op
- * (exactsample_amd/csrc/binding.cpp) and a ctypes caller both sit on top.
+ * (exactsample/csrc/binding.cpp) and a ctypes caller both sit on top.
  *
  * Semantics are the reference contract (docs/contract.md): per-request statuses,
  * -1 tokens for failed requests, Philox keyed by (seed, stream, position,

@@ -1,6 +1,6 @@
 """CPU oracle for exactsample's sampling/verification path.
 
-TEST INFRASTRUCTURE ONLY. Nothing in the product path (``exactsample_amd``)
+TEST INFRASTRUCTURE ONLY. Nothing in the product path (the ``exactsample`` package)
 imports, links or runs anything from this package. Only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` use
 it, and only as the checker or the timed CPU baseline.

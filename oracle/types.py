@@ -2,7 +2,7 @@
 
 Restates python/exactsample/types.py:7-44 (Status, PathUsed, RequestParams,
 RngKey, VerifyOutput). The product package defines the same enums itself
-(exactsample_amd/types.py); tests check the two agree.
+(exactsample/types.py); tests check the two agree.
 """
 from dataclasses import dataclass
 from enum import IntEnum

@@ -1,67 +1,85 @@
-"""Device-side setup for GPU parity tests (allocation stays outside ``verify``).
+"""GPU-side plumbing of the parity tests.
 
-Mirrors the reference's tests/cuda_helpers.py:6-46: the same inputs become
-device tensors of a chosen dtype (optionally with every last dimension
-strided by two), a plan sized for them and its output buffers. ``compare``
-then checks tokens, accepted lengths and statuses against the oracle run on
-exactly the values the device saw (after rounding to the dtype).
+``prepared`` turns one batch (NumPy logits, offsets, draft IDs, parameters,
+RNG key, optional mask and proposal logits) into the keyword arguments of
+``exactsample.cuda.verify``: device tensors in the chosen logits dtype,
+optionally with a stride of two elements in every last dimension, a plan
+sized for the batch and its output buffers. ``run_and_compare`` makes the
+call and checks tokens, accepted lengths and statuses against the oracle run
+on exactly the values the device received (after rounding to the dtype).
 """
+import struct
+
 import numpy as np
 
 from oracle import RequestParams, RngKey, verify_reference
 
 
 def packed_mask(allowed):
-    """Pack a boolean [rows, V] array into int32 words, bit t % 32 of word t // 32."""
+    """Boolean [rows, V] -> int32 words [rows, ceil(V / 32)], token t at bit t % 32 of word t // 32."""
+    allowed = np.asarray(allowed, dtype=bool)
     rows, vocab = allowed.shape
-    bits = np.zeros((rows, (vocab + 31) // 32 * 32), np.uint64)
-    bits[:, :vocab] = allowed
-    words = (bits.reshape(rows, -1, 32) << np.arange(32, dtype=np.uint64)).sum(-1)
-    return words.astype(np.uint32).view(np.int32)
+    width = -(-vocab // 32) * 32
+    bits = np.pad(allowed, ((0, 0), (0, width - vocab)))
+    return np.packbits(bits.reshape(rows, -1, 32), axis=-1, bitorder="little").view("<i4").reshape(rows, -1)
+
+
+def _on_device(value, dtype, strided):
+    """A device tensor holding `value`; with `strided`, its last dimension has element stride 2."""
+    import torch
+    host = torch.as_tensor(np.array(value), dtype=dtype)
+    if not strided or host.ndim == 0 or host.shape[-1] == 0:
+        return host.to("cuda")
+    pairs = torch.zeros((*host.shape, 2), dtype=dtype, device="cuda")
+    view = pairs[..., 0]
+    view.copy_(host)
+    return view
+
+
+def _per_request(value, requests):
+    """A scalar or per-request parameter as a list of `requests` Python values."""
+    array = np.asarray(value, dtype=object)
+    return [array.item()] * requests if array.ndim == 0 else [v for v in array]
 
 
 def prepared(logits, cu_rows, draft_ids, *, params=None, rng=None, mask=None, draft_logits=None,
              dtype=None, strided=False, reference=False):
+    """The verify() keyword arguments for one batch (see the module docstring)."""
     import torch
-    from exactsample_amd.cuda import CudaRequestParams, CudaRngKey, plan
+    from exactsample.cuda import CudaRequestParams, CudaRngKey, plan
 
     params = params or RequestParams()
-    data = np.asarray(logits)
+    logits = np.asarray(logits)
     offsets = np.asarray(cu_rows)
     ids = np.asarray(draft_ids, dtype=np.int64)
-    rows, vocab = data.shape
-    requests = len(offsets) - 1
+    rows, vocab = logits.shape
+    requests = offsets.size - 1
     rng = rng or RngKey(1234, 3, np.arange(rows))
     dtype = dtype or torch.float64
 
-    def tensor(value, kind):
-        result = torch.as_tensor(np.array(value, copy=True), dtype=kind, device="cuda")
-        if strided and result.ndim and result.shape[-1]:
-            backing = torch.empty((*result.shape[:-1], result.shape[-1] * 2), dtype=kind, device="cuda")
-            backing[..., ::2] = result
-            result = backing[..., ::2]
-        return result
+    def dev(value, kind):
+        return _on_device(value, kind, strided)
 
-    def per(value):
-        array = np.asarray(value, dtype=object)
-        return [array.item()] * requests if array.ndim == 0 else list(array)
-
-    seeds = [int(s) if int(s) < 2**63 else int(s) - 2**64 for s in per(rng.seed)]
-    gpu_params = CudaRequestParams(
-        tensor(per(params.temperature), torch.float64), tensor(per(params.top_k), torch.int64),
-        tensor(per(params.top_p), torch.float64), tensor(per(params.min_p), torch.float64),
-        tensor([0 if k == "one_hot" else 1 for k in per(params.draft_kind)], torch.int64))
-    gpu_rng = CudaRngKey(tensor(seeds, torch.int64), tensor(per(rng.stream_id), torch.int64),
-                         tensor(rng.positions, torch.int64))
+    seeds = np.array([int(s) % 2**64 for s in _per_request(rng.seed, requests)], dtype=np.uint64).view(np.int64)
+    kinds = [int(k != "one_hot") for k in _per_request(params.draft_kind, requests)]
+    device_params = CudaRequestParams(
+        temperature=dev(_per_request(params.temperature, requests), torch.float64),
+        top_k=dev(_per_request(params.top_k, requests), torch.int64),
+        top_p=dev(_per_request(params.top_p, requests), torch.float64),
+        min_p=dev(_per_request(params.min_p, requests), torch.float64),
+        draft_kind=dev(kinds, torch.int64))
+    device_rng = CudaRngKey(seed=dev(seeds, torch.int64),
+                            stream_id=dev(_per_request(rng.stream_id, requests), torch.int64),
+                            positions=dev(np.asarray(rng.positions, dtype=np.int64), torch.int64))
     work = plan(rows, requests, ids.shape[1], vocab, reference=reference)
-    args = dict(target_logits=tensor(data, dtype), cu_rows=tensor(offsets, torch.int64),
-                draft_ids=tensor(ids, torch.int64), params=gpu_params, rng=gpu_rng,
-                plan=work, out=work.allocate_output())
+    kwargs = dict(target_logits=dev(logits, dtype), cu_rows=dev(offsets, torch.int64),
+                  draft_ids=dev(ids, torch.int64), params=device_params, rng=device_rng, plan=work,
+                  out=work.allocate_output())
     if mask is not None:
-        args["mask"] = tensor(mask, torch.int32)
+        kwargs["mask"] = dev(mask, torch.int32)
     if draft_logits is not None:
-        args["draft_logits"] = tensor(draft_logits, dtype)
-    return args
+        kwargs["draft_logits"] = dev(draft_logits, dtype)
+    return kwargs
 
 
 def expected_for(args, offsets, ids, *, params=None, rng=None, mask=None, mode="ratio"):
@@ -75,7 +93,7 @@ def expected_for(args, offsets, ids, *, params=None, rng=None, mask=None, mode="
 def run_and_compare(logits, offsets, ids, *, params=None, rng=None, mask=None, draft_logits=None, mode="ratio",
                     dispatch="fused", dtype=None, strided=False, list_max=256, top_k_top_p=True):
     """Runs one call, checks it against the oracle and returns (out, fallbacks, args)."""
-    from exactsample_amd.cuda import verify
+    from exactsample.cuda import verify
 
     rng = rng or RngKey(1234, 3, np.arange(len(logits)))
     args = prepared(logits, offsets, ids, params=params, rng=rng, mask=mask, draft_logits=draft_logits,
@@ -96,9 +114,9 @@ def run_and_compare(logits, offsets, ids, *, params=None, rng=None, mask=None, d
 def row_diagnostics(plan, rows):
     """(route, fallbacks) of each row of the plan's last call, read from the workspace.
 
-    route: 1 failed, 2 greedy, 3 top-k list, 4 top-p list, 5 full-row path.
+    route: 1 failed, 2 greedy, 3 top-k list, 4 top-p list, 5 streaming draw,
+    100 + reason: the full-row path.
     """
-    import struct
     plan.synchronize()
     data = plan.workspace.cpu().numpy().tobytes()
     out = []

@@ -7,7 +7,7 @@ from pathlib import Path
 
 import pytest
 
-from exactsample_amd import capi
+from exactsample import capi
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "exactsample_amd.h"
@@ -15,9 +15,9 @@ HEADER = ROOT / "include" / "exactsample_amd.h"
 
 @pytest.fixture(scope="module")
 def lib():
-    path = ROOT / "exactsample_amd" / "libexactsample_amd.so"
+    path = ROOT / "exactsample" / "libexactsample_amd.so"
     if not path.is_file():
-        pytest.skip("libexactsample_amd.so is not built (python -m exactsample_amd.build)")
+        pytest.skip("libexactsample_amd.so is not built (python -m exactsample.build)")
     return capi.load(path)
 
 
@@ -94,3 +94,20 @@ def test_null_arguments_and_empty_batch(lib):
     a = arguments(rows=0, requests=0)
     a.target = capi.Matrix(None, 0, 0, 0, 0)
     assert lib.es_launch(ctypes.byref(a), None) == 0  # nothing to do, nothing launched
+
+
+@pytest.mark.parametrize("dtype, vocab, list_max", [(2, 262148, 256), (0, 300000, 0), (3, 1048580, 256),
+                                                    (1, 2**31 - 1, 256)])
+def test_any_vocabulary_passes_the_host_checks(lib, dtype, vocab, list_max):
+    """Vocabularies past 64 register tiles per row are accepted (slices of
+    several tiles): without a device the call gets as far as the launch and
+    reports ES_ERR_LAUNCH, never ES_ERR_BAD_DIMENSION. Run only where no HIP
+    device is visible, since the addresses here are fake."""
+    import torch
+    if torch.cuda.device_count() > 0:
+        pytest.skip("a HIP device is visible: the fake addresses must not reach a kernel")
+    a = arguments(rows=3, requests=3, vocab=vocab, max_draft=0)
+    a.target = capi.Matrix(1 << 20, vocab, 1, dtype, 0)
+    a.list_max = list_max
+    a.workspace_bytes = lib.es_workspace_size(3, vocab, 0)
+    assert lib.es_launch(ctypes.byref(a), None) == 7

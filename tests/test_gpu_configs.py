@@ -16,12 +16,12 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture(autouse=True)
 def _device(hip_device):
-    from exactsample_amd.cuda import load_library
+    from exactsample.cuda import load_library
     load_library()
 
 
 def _run(work, list_max=None):
-    from exactsample_amd.cuda import verify
+    from exactsample.cuda import verify
 
     args = bench.device_args(work)
     if list_max is not None:
@@ -70,7 +70,7 @@ def test_slice_maxima_in_the_last_group():
 
 
 def test_greedy_and_plain_temperature_rows():
-    from exactsample_amd.cuda import CudaRequestParams, verify
+    from exactsample.cuda import CudaRequestParams, verify
     import torch
     work = bench.config2(seed=5)
     temps = np.where(np.arange(128) % 2 == 0, 0.0, 1.0)

@@ -20,7 +20,7 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture(autouse=True)
 def _device(hip_device):
-    from exactsample_amd.cuda import load_library
+    from exactsample.cuda import load_library
     load_library()  # a missing library on a GPU box is a failure, not a skip
 
 
@@ -96,7 +96,7 @@ def test_coupled_matches_ordinary_and_reordered_batch():
 
 def test_workspace_conflict_and_separate_plans():
     import torch
-    from exactsample_amd.cuda import verify
+    from exactsample.cuda import verify
     if not hasattr(torch.cuda, "_sleep"):
         pytest.skip("torch.cuda._sleep unavailable for the in-flight fixture")
     args = prepared(np.zeros((1, 4)), [0, 1], np.empty((1, 0), np.int64))
@@ -118,7 +118,7 @@ def test_workspace_conflict_and_separate_plans():
 
 def test_capacity_failure_and_large_k():
     import torch
-    from exactsample_amd.cuda import verify
+    from exactsample.cuda import verify
     out, _, _ = run_and_compare(np.zeros((1, 100)), [0, 1], np.empty((1, 0), np.int64),
                                 params=RequestParams(top_k=65))
     assert out.path_used.cpu().tolist() == [1]
@@ -136,7 +136,7 @@ def test_rng_boundaries():
 
 
 def test_output_alias_is_rejected():
-    from exactsample_amd.cuda import verify
+    from exactsample.cuda import verify
     args = prepared(np.zeros((1, 4)), [0, 1], np.empty((1, 0), np.int64))
     args["out"].tokens = args["rng"].seed.reshape(1, 1)
     with pytest.raises(RuntimeError, match="alias"):
@@ -145,7 +145,7 @@ def test_output_alias_is_rejected():
 
 def test_noncontiguous_outputs():
     import torch
-    from exactsample_amd.cuda import verify
+    from exactsample.cuda import verify
     args = prepared(np.zeros((3, 4)), [0, 1, 3], [[-1], [2]], strided=True)
     out = args["out"]
     backing = torch.full((2, 4), -777, dtype=torch.int64, device="cuda")
@@ -160,7 +160,7 @@ def test_noncontiguous_outputs():
 
 @pytest.mark.parametrize("offsets", [[1, 1, 2], [0, 2, 1], [0, -1, 2], [0, 1, 3]])
 def test_malformed_offsets_make_every_request_invalid(offsets):
-    from exactsample_amd.cuda import verify
+    from exactsample.cuda import verify
     args = prepared(np.zeros((2, 4)), offsets, np.empty((2, 0), np.int64))
     out = verify(**args)
     args["plan"].synchronize()
@@ -179,7 +179,7 @@ def test_requests_without_rows_are_invalid():
     # No rows at all: only the request checks run (reference: verify.cu:6-56,
     # a segment of 1..max_draft+1 rows). The recompute count is cleared too.
     import torch
-    from exactsample_amd.cuda import CudaRequestParams, CudaRngKey, plan, verify
+    from exactsample.cuda import CudaRequestParams, CudaRngKey, plan, verify
     work = plan(4, 4, 1, 8)
     work.workspace.fill_(0xff)  # stale header words from an earlier call
     out = work.allocate_output()
@@ -198,7 +198,7 @@ def test_requests_without_rows_are_invalid():
 
 def test_empty_batch_is_valid():
     import torch
-    from exactsample_amd.cuda import CudaRequestParams, CudaRngKey, plan, verify
+    from exactsample.cuda import CudaRequestParams, CudaRngKey, plan, verify
     work = plan(4, 4, 1, 8)
     out = work.allocate_output()
     z64 = torch.zeros(0, dtype=torch.int64, device="cuda")

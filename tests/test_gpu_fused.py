@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture(autouse=True)
 def _device(hip_device):
-    from exactsample_amd.cuda import load_library
+    from exactsample.cuda import load_library
     load_library()
 
 
@@ -170,7 +170,7 @@ def test_real_vocabulary_with_mask():
 
 def test_batch_invariance():
     import torch
-    from exactsample_amd.cuda import verify
+    from exactsample.cuda import verify
     g = np.random.default_rng(3)
     vocab, counts = 1000, [0, 3, 1, 2, 0]
     params = dict(temperature=[.7, 1., 0., .5, 1.2], top_k=[0, 20, 0, 400, 5], top_p=[.95, .9, 1., 1., .8],

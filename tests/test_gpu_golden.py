@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture(autouse=True)
 def _device(hip_device):
-    from exactsample_amd.cuda import load_library
+    from exactsample.cuda import load_library
     load_library()
 
 
@@ -23,7 +23,7 @@ def _device(hip_device):
 @pytest.mark.parametrize("list_max", [256, 0])
 def test_captured_logits_match_reference_outputs(name, requests, drafts, list_max):
     import torch
-    from exactsample_amd.cuda import CudaRequestParams, CudaRngKey, plan, verify
+    from exactsample.cuda import CudaRequestParams, CudaRngKey, plan, verify
 
     capture = cap.load_capture()
     rows, offsets, ids, seeds, streams, positions = cap.workload(capture, requests, drafts)

@@ -27,7 +27,7 @@ def drafts_of(kind):
 @pytest.mark.parametrize("name", list(CELLS))
 def test_recorded_counts(name, list_max, hip_device):
     import torch
-    from exactsample_amd.cuda import CudaRequestParams, CudaRngKey, load_library, plan, verify
+    from exactsample.cuda import CudaRequestParams, CudaRngKey, load_library, plan, verify
 
     load_library()
     cell = CELLS[name]

@@ -1,7 +1,7 @@
 """The FP32 Gumbel noise of the certified draws, checked over all 2^32 Philox words.
 
 The draws prune and certify with three facts about gumbel32 / gumbel_upper
-(exactsample_amd/csrc/es_device.h) that depend on the device's logf, log1pf
+(exactsample/csrc/es_device.h) that depend on the device's logf, log1pf
 and __logf: |gumbel32(w) - G(w)| <= 2^-19 (1 + |G|), gumbel_upper(w) >= G(w),
 and G(w) < 22.875, with G = -log(-log u), u = (w + 0.5) / 2^32, in FP64. The
 library's es_check_gumbel makes the three checks on the device (the role of
@@ -15,7 +15,7 @@ import struct
 import numpy as np
 import pytest
 
-from exactsample_amd import capi
+from exactsample import capi
 
 
 def from_key(k):
