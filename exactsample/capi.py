@@ -48,8 +48,9 @@ class Arguments(ctypes.Structure):
     ]
 
 
-EXPORTS = ["es_workspace_size", "es_launch", "es_error_string", "es_last_hip_error", "es_set_split_event",
-           "es_check_gumbel", "es_fallback_counter_offset"]
+EXPORTS = ["es_workspace_size", "es_launch", "es_launch_static", "es_error_string", "es_last_hip_error",
+           "es_set_split_event", "es_check_gumbel", "es_fallback_counter_offset"]
+STATIC_WORKSPACE_BYTES = 16 << 20  # ES_STATIC_WORKSPACE_BYTES
 
 
 def load(path=None):
@@ -69,6 +70,8 @@ def load(path=None):
     lib.es_workspace_size.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32]
     lib.es_launch.restype = ctypes.c_int32
     lib.es_launch.argtypes = [ctypes.POINTER(Arguments), ctypes.c_void_p]
+    lib.es_launch_static.restype = ctypes.c_int32
+    lib.es_launch_static.argtypes = [ctypes.POINTER(Arguments), ctypes.c_void_p]
     lib.es_error_string.restype = ctypes.c_char_p
     lib.es_error_string.argtypes = [ctypes.c_int32]
     lib.es_last_hip_error.restype = ctypes.c_char_p
@@ -114,10 +117,12 @@ def from_tensors(target_logits, cu_rows, draft_ids, draft_logits, temperature, t
     return a
 
 
-def launch(lib, args, stream=None):
-    """es_launch on `stream` (a HIP stream handle or a torch stream); raises on an error code."""
+def launch(lib, args, stream=None, static_workspace=False):
+    """es_launch (or, with `static_workspace`, es_launch_static) on `stream` (a HIP
+    stream handle or a torch stream); raises on an error code."""
     handle = getattr(stream, "cuda_stream", stream)
-    code = lib.es_launch(ctypes.byref(args), ctypes.c_void_p(handle or 0))
+    entry = lib.es_launch_static if static_workspace else lib.es_launch
+    code = entry(ctypes.byref(args), ctypes.c_void_p(handle or 0))
     if code != 0:
         detail = lib.es_last_hip_error().decode()
         raise RuntimeError(f"es_launch failed: {lib.es_error_string(code).decode()}" + (f" ({detail})" if detail else ""))

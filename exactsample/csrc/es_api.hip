@@ -2,6 +2,7 @@
 // (include/exactsample_amd.h).
 #include <limits.h>
 #include <atomic>
+#include <mutex>
 #include <stdio.h>
 #include "es_layout.h"
 #include "es_plan.h"
@@ -77,6 +78,8 @@ const char* es_error_string(int32_t code) {
     case ES_ERR_WORKSPACE_ALIGN: return "workspace alignment must be 8 bytes";
     case ES_ERR_BAD_DTYPE: return "unsupported logits dtype (draft logits must match the target dtype)";
     case ES_ERR_LAUNCH: return "exactsample kernel launch failed";
+    case ES_ERR_STATIC_CAPACITY:
+      return "the call needs more than the library's static workspace (ES_STATIC_WORKSPACE_BYTES: 8 + rows x 12320 bytes)";
     default: return "unknown exactsample_amd error";
   }
 }
@@ -85,9 +88,14 @@ const char* es_last_hip_error(void) { return g_last_hip_error; }
 
 void es_set_split_event(void* event) { g_split_event = static_cast<hipEvent_t>(event); }
 
-int32_t es_launch(const es_arguments* args, void* stream_ptr) {
-  if (!args) return ES_ERR_NULL_ARGUMENT;
-  const es_arguments& a = *args;
+}  // extern "C"
+
+namespace {
+
+// es_launch's checks and launches. With `own_workspace` the workspace is the
+// library's static array (set by the caller), so the caller's workspace
+// fields are neither required nor checked.
+int32_t launch_call(const es_arguments& a, void* stream_ptr, bool own_workspace) {
   g_last_hip_error[0] = 0;
   if (a.requests < 0 || a.rows < 0 || a.vocab <= 0 || a.vocab > INT32_MAX || a.rows > 65535 ||
       a.requests > INT32_MAX || a.max_draft < 0 || a.max_draft >= INT32_MAX)
@@ -104,9 +112,11 @@ int32_t es_launch(const es_arguments* args, void* stream_ptr) {
     return ES_ERR_NULL_ARGUMENT;
   if (a.target.dtype < ES_F32 || a.target.dtype > ES_BF16) return ES_ERR_BAD_DTYPE;
   if (a.draft.data && a.draft.dtype != a.target.dtype) return ES_ERR_BAD_DTYPE;
-  const size_t need = es_workspace_size(a.rows, a.vocab, a.dispatch == 1);
-  if (need == 0 || a.workspace_bytes < need) return ES_ERR_WORKSPACE_SIZE;
-  if (reinterpret_cast<uintptr_t>(a.workspace) % 8 != 0) return ES_ERR_WORKSPACE_ALIGN;
+  if (!own_workspace) {
+    const size_t need = es_workspace_size(a.rows, a.vocab, a.dispatch == 1);
+    if (need == 0 || a.workspace_bytes < need) return ES_ERR_WORKSPACE_SIZE;
+    if (reinterpret_cast<uintptr_t>(a.workspace) % 8 != 0) return ES_ERR_WORKSPACE_ALIGN;
+  }
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   // dispatch 1 ("reference"): every row is finished on the exact full-row
   // path, so the slices gather no list candidates.
@@ -153,6 +163,61 @@ int32_t es_launch(const es_arguments* args, void* stream_ptr) {
     return ES_ERR_LAUNCH;
   }
   return ES_SUCCESS;
+}
+
+// The workspace of es_launch_static: one copy per GPU, held until the process
+// ends. Host code never uses this name as an address (on the host it is a
+// stand-in); the device address of each GPU's copy comes from
+// hipGetSymbolAddress, once per device, with that device current.
+static __device__ __align__(256) uint8_t scratch[ES_STATIC_WORKSPACE_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+uint8_t* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of `scratch` (looked up on the device's first call).
+int32_t scratch_of_current_device(uint8_t** out) {
+  int device = -1;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) {
+    es::note_hip_error(err);
+    return ES_ERR_LAUNCH;
+  }
+  if (device < 0 || device >= kMaxDevices) return ES_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[device]) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr) {
+      es::note_hip_error(err);
+      return ES_ERR_LAUNCH;
+    }
+    g_scratch_ptr[device] = static_cast<uint8_t*>(ptr);
+  }
+  *out = g_scratch_ptr[device];
+  return ES_SUCCESS;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t es_launch(const es_arguments* args, void* stream_ptr) {
+  if (!args) return ES_ERR_NULL_ARGUMENT;
+  return launch_call(*args, stream_ptr, false);
+}
+
+int32_t es_launch_static(const es_arguments* args, void* stream_ptr) {
+  if (!args) return ES_ERR_NULL_ARGUMENT;
+  // The rows' regions, whatever the dispatch: the kernels use 8 + rows * 12,320 bytes.
+  const size_t need = es_workspace_size(args->rows, args->vocab, 0);
+  if (args->rows < 0 || args->vocab <= 0 || need == 0) return ES_ERR_BAD_DIMENSION;
+  if (need > ES_STATIC_WORKSPACE_BYTES) return ES_ERR_STATIC_CAPACITY;
+  es_arguments run = *args;
+  const int32_t found = scratch_of_current_device(&run.workspace);
+  if (found != ES_SUCCESS) return found;
+  run.workspace_bytes = ES_STATIC_WORKSPACE_BYTES;
+  return launch_call(run, stream_ptr, true);
 }
 
 }  // extern "C"

@@ -34,7 +34,8 @@ enum es_error {
   ES_ERR_WORKSPACE_SIZE = 4,    /* workspace smaller than es_workspace_size() */
   ES_ERR_WORKSPACE_ALIGN = 5,   /* workspace not 8-byte aligned */
   ES_ERR_BAD_DTYPE = 6,         /* unknown es_dtype, or draft dtype differs from target */
-  ES_ERR_LAUNCH = 7             /* the HIP runtime refused a kernel launch */
+  ES_ERR_LAUNCH = 7,            /* the HIP runtime refused a kernel launch */
+  ES_ERR_STATIC_CAPACITY = 8    /* es_launch_static: the call needs more than ES_STATIC_WORKSPACE_BYTES */
 };
 
 /* A [rows, vocab] logits matrix with element strides; replaces exactsample::Matrix (api.h:11-15). */
@@ -87,6 +88,25 @@ size_t es_workspace_size(int64_t rows, int64_t vocab, int32_t reference);
  * allocates, never synchronizes. Replaces exactsample::launch (api.h:44,
  * csrc/verify/verify.cu:220-228). Returns an es_error code. */
 int32_t es_launch(const es_arguments* args, void* stream);
+
+/* Bytes of the library's own per-GPU workspace used by es_launch_static: room
+ * for 8 + rows * 12320 bytes, i.e. up to 1,361 rows of any vocabulary. */
+#define ES_STATIC_WORKSPACE_BYTES (16u << 20)
+
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): es_launch with the workspace replaced by a file-scope
+ * device array of ES_STATIC_WORKSPACE_BYTES in this library, one copy per GPU
+ * held until the process ends (its address is looked up on the device's first
+ * call). args->workspace and args->workspace_bytes are ignored; the caller
+ * still passes inputs and outputs. Calls needing more than the array (rows
+ * above 1,361) return ES_ERR_STATIC_CAPACITY before any HIP call. No call
+ * allocates or frees memory. No byte of the array needs a particular value
+ * when a call starts. Every call on one GPU shares that GPU's array: calls
+ * that overlap on one GPU (on different streams, or from several host
+ * threads) race and must not be issued. The FP64 recomputation count of the
+ * last call is not exposed. */
+int32_t es_launch_static(const es_arguments* args, void* stream);
 
 /* A static description of an es_error code. */
 const char* es_error_string(int32_t code);
