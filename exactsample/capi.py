@@ -49,7 +49,7 @@ class Arguments(ctypes.Structure):
 
 
 EXPORTS = ["es_workspace_size", "es_launch", "es_launch_static", "es_error_string", "es_last_hip_error",
-           "es_set_split_event", "es_check_gumbel", "es_fallback_counter_offset"]
+           "es_set_split_event", "es_check_gumbel", "es_check_weights", "es_fallback_counter_offset"]
 STATIC_WORKSPACE_BYTES = 16 << 20  # ES_STATIC_WORKSPACE_BYTES
 
 
@@ -78,6 +78,8 @@ def load(path=None):
     lib.es_last_hip_error.argtypes = []
     lib.es_check_gumbel.restype = ctypes.c_int32
     lib.es_check_gumbel.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p]
+    lib.es_check_weights.restype = ctypes.c_int32
+    lib.es_check_weights.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p]
     lib.es_set_split_event.restype = None
     lib.es_set_split_event.argtypes = [ctypes.c_void_p]
     lib.es_fallback_counter_offset.restype = ctypes.c_size_t

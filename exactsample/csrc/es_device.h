@@ -185,6 +185,23 @@ __device__ __forceinline__ float gumbel_upper(uint32_t w) {
 }
 
 // ---------------------------------------------------------------------------
+// Temperature arithmetic and FP32 weights, with the bounds the certified
+// decisions use (checked on the device by es_check_weights):
+//  - formation: |x32 - x| <= X_ERR_FORM |x| + 2^-126 for x32 = Temp::x32(v)
+//    and the oracle's x = (l - max) / T in FP64 (three FP32 roundings: the
+//    difference, 1 / T and the product, each within 2^-24);
+//  - weights: |weight32(x) / exp(x) - 1| <= X_ERR_EXP for every FP32 x in
+//    [-40, 0] (all 1.1e9 of them);
+//  - together: |weight32(x32) / exp(x) - 1| <= X_ERR (1 + |x|), since
+//    X_ERR_EXP + 1.0001 X_ERR_FORM |x| <= X_ERR (1 + |x|).
+constexpr float X_ERR = 4.8e-7f;        // |x32 - x| <= X_ERR * |x|; |w32/w - 1| <= X_ERR * (1 + |x|)
+constexpr double X_ERR_FORM = 1.8e-7;   // 3 * 2^-24, rounded up
+constexpr double X_ERR_EXP = 2.9e-7;    // X_ERR - X_ERR_FORM, rounded down
+
+// The FP32 weight of an FP32 x (the library's expf, as every FP32 sum uses it).
+__device__ __forceinline__ float weight32(float x) { return expf(x); }
+
+// ---------------------------------------------------------------------------
 // Unsigned keys in value order; -0 and +0 get the same key (the oracle compares
 // values, and -0 == +0).
 __device__ __forceinline__ uint32_t order_key(float v) {
@@ -238,5 +255,40 @@ __device__ __forceinline__ bool dd_round_certain(DD s, double err, double* out) 
 __device__ __forceinline__ double dd_sum_error(DD s, double n) {
   return n * 0x1p-100 * s.hi + n * 0x1p-1060;
 }
+
+// Temperature arithmetic shared by the slice pass, the list and the full-row
+// parts.
+template <class W> struct Temp {
+  double M, T, min_p;
+  float inv_t, ln_min_p, min_p_tol;
+  bool slow;
+  __device__ __forceinline__ void init(double maximum, double temperature, double min_p_) {
+    M = maximum; T = temperature; min_p = min_p_;
+    inv_t = float(1.0 / temperature);
+    slow = !(inv_t < 1e30f);
+    ln_min_p = min_p > 0 ? float(log(min_p)) : -INFINITY;
+    min_p_tol = min_p > 0 ? 1e-6f * (1.f + fabsf(ln_min_p)) : 0.f;
+  }
+  // The oracle's x = (l - max) / T in FP64 (reference.py:63).
+  __device__ __forceinline__ double x64(W v) const { return (double(v) - M) / T; }
+  // FP32 x with |x32 - x| <= X_ERR_FORM * |x| + 2^-126.
+  __device__ __forceinline__ float x32(W v) const {
+    if constexpr (sizeof(W) == 8) {
+      return float(x64(v));
+    } else {
+      const float d = v - float(M);
+      return slow ? float(double(d) / T) : d * inv_t;
+    }
+  }
+  // exp(x) >= min_p and exp(x) > 0 for the FP64 x, settled in FP32 when x is
+  // clear of both thresholds and in FP64 otherwise. The margin X_ERR |x| +
+  // min_p_tol covers x32's formation error and ln_min_p's rounding.
+  __device__ __forceinline__ bool kept(W v, float x) const {
+    if (x > -744.f && fabsf(x - ln_min_p) > X_ERR * fabsf(x) + min_p_tol) return x > ln_min_p;
+    if (x < -745.2f) return false;
+    const double w = exp(x64(v));
+    return w > 0 && w >= min_p;
+  }
+};
 
 }  // namespace es

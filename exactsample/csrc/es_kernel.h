@@ -43,7 +43,6 @@
 
 namespace es {
 
-constexpr float X_ERR = 4.8e-7f;          // |x32 - x| <= X_ERR * |x|; |w32/w - 1| <= X_ERR * (1 + |x|)
 constexpr float SCORE_ERR = 1.9073486e-06f;  // |s32 - s| <= SCORE_ERR * (1 + |x| + |G|)
 constexpr float PRUNE_MARGIN = 1e-3f;
 constexpr float SUM_PRUNE = -40.f;        // weights below e^-40 are bounded, not summed
@@ -665,40 +664,6 @@ __device__ __forceinline__ void skip_row(const es_arguments& a, int64_t row) {
     st->fallbacks = 0;
   }
 }
-
-// ---------------------------------------------------------------------------
-// Temperature arithmetic shared by the list and full-row parts.
-template <class W> struct Temp {
-  double M, T, min_p;
-  float inv_t, ln_min_p, min_p_tol;
-  bool slow;
-  __device__ __forceinline__ void init(double maximum, double temperature, double min_p_) {
-    M = maximum; T = temperature; min_p = min_p_;
-    inv_t = float(1.0 / temperature);
-    slow = !(inv_t < 1e30f);
-    ln_min_p = min_p > 0 ? float(log(min_p)) : -INFINITY;
-    min_p_tol = min_p > 0 ? 1e-6f * (1.f + fabsf(ln_min_p)) : 0.f;
-  }
-  // The oracle's x = (l - max) / T in FP64 (reference.py:63).
-  __device__ __forceinline__ double x64(W v) const { return (double(v) - M) / T; }
-  // FP32 x with |x32 - x| <= X_ERR * |x|.
-  __device__ __forceinline__ float x32(W v) const {
-    if constexpr (sizeof(W) == 8) {
-      return float(x64(v));
-    } else {
-      const float d = v - float(M);
-      return slow ? float(double(d) / T) : d * inv_t;
-    }
-  }
-  // exp(x) >= min_p and exp(x) > 0 for the FP64 x, settled in FP32 when x is
-  // clear of both thresholds and in FP64 otherwise.
-  __device__ __forceinline__ bool kept(W v, float x) const {
-    if (x > -744.f && fabsf(x - ln_min_p) > X_ERR * fabsf(x) + min_p_tol) return x > ln_min_p;
-    if (x < -745.2f) return false;
-    const double w = exp(x64(v));
-    return w > 0 && w >= min_p;
-  }
-};
 
 // ---------------------------------------------------------------------------
 // Composite order keys: larger means earlier in (logit desc, ID asc) order.
@@ -1681,7 +1646,7 @@ template <int DT, bool VEC> struct FullRow {
             if (!in_final(t, v, ok)) return;
             const float x = tp.x32(v);
             if (x < SUM_PRUNE) { ++pruned; return; }
-            const float w = expf(x), d = w - c, tt = s + d;
+            const float w = weight32(x), d = w - c, tt = s + d;
             c = (tt - s) - d; s = tt;
             e += w * (X_ERR * (1.f + fabsf(x)));
           });
@@ -1774,7 +1739,7 @@ struct KahanSum {
   int pruned = 0;
   __device__ __forceinline__ void add(float x) {
     if (!(x >= SUM_PRUNE)) { ++pruned; return; }
-    const float w = expf(x), d = w - c, t = s + d;
+    const float w = weight32(x), d = w - c, t = s + d;
     c = (t - s) - d;
     s = t;
     e += w * (X_ERR * (1.f + fabsf(x)));

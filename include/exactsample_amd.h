@@ -133,6 +133,21 @@ void es_set_split_event(void* event);
  * (key k: FP64 bits k & ~2^63 if k >= 2^63, else ~k). Enqueued on `stream`. */
 int32_t es_check_gumbel(uint64_t first_word, uint64_t count, uint64_t* report, void* stream);
 
+/* Device self-test with no counterpart in the reference's API, of the bound
+ * the certified FP32 sums and min-p decisions use (the reference states it as
+ * X_ERR, csrc/verify/fused.cuh:62-67, for its CUDA expf): over indices
+ * [first_index, first_index + count) of [0, 2^32), index i <= 0x42200000 checks
+ * the FP32 x with bits 0x80000000 | i (every FP32 x in [-40, 0] over the whole
+ * range): |weight32(x) / exp(x) - 1| <= 2.9e-7; every index also checks a
+ * pseudo-random (v, M, T): |x32 - x| <= 1.8e-7 |x| + 2^-126 for x32 as the
+ * kernels form it and x = (v - M) / T in FP64, and, for x in [-40, 0],
+ * |weight32(x32) / exp(x) - 1| <= 4.8e-7 (1 + |x|). `report` is 8 device
+ * uint64 words, overwritten: indices checked, weight violations, formation
+ * violations, combined violations, then as FP64 bits the largest weight error,
+ * the largest |x32 - x| / |x| and the largest combined error / bound, then
+ * the count of FP32 x checked. Enqueued on `stream`. */
+int32_t es_check_weights(uint64_t first_index, uint64_t count, uint64_t* report, void* stream);
+
 /* Offset of the FP64 recomputation counter in the workspace (a uint32 written by
  * each call; read it after the call completes). Replaces workspace word 1 read at
  * python/exactsample/cuda.py:109-114. */

@@ -71,3 +71,43 @@ def test_all_words_on_the_device(hip_device):
     assert (bad_error, bad_screen, bad_range) == (0, 0, 0)
     assert worst <= 1.0 and slack >= 0.0
     assert hi == pytest.approx(noise(2**32 - 1), rel=1e-14) and lo == pytest.approx(noise(0), rel=1e-14)
+
+
+def test_weight_check_rejects_bad_ranges_without_a_launch():
+    lib = capi.load()
+    fake = ctypes.c_void_p(1 << 20)
+    assert lib.es_check_weights(0, 1, None, None) == 1
+    assert lib.es_check_weights(2**32 + 1, 0, fake, None) == 2
+    assert lib.es_check_weights(0, 1, ctypes.c_void_p((1 << 20) + 4), None) == 5
+
+
+@pytest.mark.gpu
+def test_fp32_weights_and_their_bound_on_the_device(hip_device):
+    """Every FP32 x in [-40, 0]: |expf(x) / exp(x) - 1| <= 2.9e-7; and 2^31
+    pseudo-random (v, M, T): the x32 formation within 1.8e-7 |x| and the
+    certified sums' bound |expf(x32) / exp(x) - 1| <= X_ERR (1 + |x|), X_ERR =
+    4.8e-7 (the constant the kernels certify FP32 kept masses and min-p
+    decisions with)."""
+    import torch
+
+    lib = capi.load()
+    report = torch.empty(8, dtype=torch.int64, device="cuda")
+    stream = torch.cuda.current_stream()
+    chunk, total = 1 << 29, 1 << 31
+    sums = np.zeros(5, dtype=np.uint64)
+    worst = [0.0, 0.0, 0.0]
+    for first in range(0, total, chunk):
+        code = lib.es_check_weights(first, chunk, ctypes.c_void_p(report.data_ptr()),
+                                    ctypes.c_void_p(stream.cuda_stream))
+        assert code == 0, (lib.es_error_string(code), lib.es_last_hip_error())
+        words = [int(x) & ((1 << 64) - 1) for x in report.cpu().tolist()]
+        sums += np.array(words[:4] + [words[7]], dtype=np.uint64)
+        for j in range(3):
+            worst[j] = max(worst[j], struct.unpack("<d", struct.pack("<Q", words[4 + j]))[0])
+        print(f"indices [{first}, {first + chunk}): expf error <= {worst[0]:.3g}, formation <= {worst[1]:.3g} |x|, "
+              f"combined <= {worst[2]:.4f} of the bound", flush=True)
+    checked, bad_exp, bad_form, bad_comb, n_exp = (int(x) for x in sums)
+    assert checked == total
+    assert n_exp == 0x42200001  # every FP32 x from -0 to -40
+    assert (bad_exp, bad_form, bad_comb) == (0, 0, 0)
+    assert worst[0] <= 2.9e-7 and worst[1] <= 1.8e-7 and worst[2] <= 1.0
