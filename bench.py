@@ -7,11 +7,15 @@ resident in HBM. The headline workload (value) is 128 requests x 1 row of
 V = 151,936 fp32 logits at T=0.6, top-k 20, top-p 0.95; the second cell is 64
 requests x (4 one-hot drafts + bonus) verified in ratio mode with the same
 settings. By default the same two batches are also timed as bfloat16 logits
-(the dtype of the reference's own benchmark), and both shapes are timed at the
-reference benchmark's other two settings, T = 1.0 and T = 0.7 top-p 0.9.
+(the dtype of the reference's own benchmark), both shapes at the reference
+benchmark's other two settings (T = 1.0, and T = 0.7 top-p 0.9), and the other
+configurations: 8 rows at T = 1; the flatness rows (sigma ~ U(0.5, 4)) at
+T = 0.7 with top-p 0.9 or min-p 0.05, in batches of 128 and 1; and the ragged
+256-request verification batch with masks and full proposals.
 Rows come from the peaked generator: base N(mu, sigma^2) with
 mu ~ U(-5, 0), sigma ~ U(2, 4); one token + U(6, 14); 15 tokens + U(0, 8);
-every even row rounded to the bf16 grid (values stay fp32).
+every even row of the two headline shapes rounded to the bf16 grid (values
+stay fp32).
 
 Reported per cell, with every timed call queued behind a spin kernel so that
 calls run back to back and events hold GPU time only: the median and mean time
@@ -19,14 +23,15 @@ per call through the C ABI (the value), the same through the torch op (which
 also records the plan's completion event), the slice-stream kernel (es_main)
 and the per-row finishing kernel (es_finish) timed apart by an event the
 library records between them, and cold medians after a 2 GiB read that evicts
-the 256 MB Infinity Cache. The roofline is es_main's: algorithmic bytes (one
-read of every logit row, plus parameters and outputs, < 0.1%) over its average
-warm duration; ``traffic`` is its HBM bytes per launch from the committed
-FETCH_SIZE / WRITE_SIZE counter summary. A plain copy kernel of the headline
-logits' size is timed first (the stream-copy rate measured on the device, and
-the counters' calibration). ``cpu_baseline`` times the FP64 oracle (oracle/,
-the reference algorithm with its per-token scalar Philox) on a bounded sample
-of the headline rows, single threaded.
+the 256 MB Infinity Cache. The roofline is the headline call's, cold:
+algorithmic bytes (one read of every logit row, plus parameters and outputs,
+< 0.1%) over the cold call's median time; warm call and es_main fractions are
+reported beside it. ``traffic`` is es_main's HBM bytes per launch from the
+committed FETCH_SIZE / WRITE_SIZE counter summary. A plain copy kernel of the
+headline logits' size is timed first (the stream-copy rate measured on the
+device, and the counters' calibration). ``cpu_baseline`` times the FP64 oracle
+(oracle/, the reference algorithm with its per-token scalar Philox) on a
+bounded sample of the headline rows, single threaded, and names the host CPU.
 """
 import argparse
 import json
@@ -136,6 +141,17 @@ def config3(seed=3, requests=128, filt="top_p"):
                 params=params, mode="ratio")
 
 
+def config3_single(seed=3, filt="top_p", row=1):
+    """Batch 1 of the flatness configuration: row `row` of its 128-row batch
+    alone (rows 0, 10, 20, ... are the constructed ones), with that row's key."""
+    work = config3(seed=seed, requests=128, filt=filt)
+    keys = work["keys"]
+    return dict(rows=work["rows"][row:row + 1].copy(), offsets=np.array([0, 1], dtype=np.int64),
+                ids=np.full((1, 1), -1, dtype=np.int64), params=work["params"], mode="ratio",
+                keys=dict(seed=keys["seed"][row:row + 1], stream=keys["stream"][row:row + 1],
+                          positions=keys["positions"][row:row + 1]))
+
+
 def config5(seed=5, requests=256, variant="full_ratio"):
     """Ragged verification: draft lengths ~ U{0..7}, a mask allowing a random
     10% of each row, filters by request {temperature only, top-k 4096, top-p
@@ -197,7 +213,18 @@ CELLS = {
     "64x5_T1": lambda: with_params(config4(), temperature=1.0, top_k=0, top_p=1.0),
     "128x1_T0.7_p0.9": lambda: with_params(config2(), temperature=0.7, top_k=0, top_p=0.9),
     "64x5_T0.7_p0.9": lambda: with_params(config4(), temperature=0.7, top_k=0, top_p=0.9),
+    # The other configurations: 8 rows at T = 1; the flatness rows (sigma ~
+    # U(0.5, 4), T = 0.7) with top-p 0.9 or min-p 0.05 in batches of 128 and
+    # 1 (row 1 of the 128-row batch: rows 0, 10, 20, ... are the constructed
+    # ones); the full ragged verification batch with full proposals.
+    "cfg1_8x1_T1": config1,
+    "cfg3_128_p0.9": lambda: config3(filt="top_p"),
+    "cfg3_128_minp0.05": lambda: config3(filt="min_p"),
+    "cfg3_1_p0.9": lambda: config3_single(filt="top_p"),
+    "cfg3_1_minp0.05": lambda: config3_single(filt="min_p"),
+    "cfg5_256_full_ratio": lambda: config5(variant="full_ratio"),
 }
+DEFAULT_CELLS = ",".join(CELLS)
 
 
 def packed_mask(allowed):
@@ -242,14 +269,20 @@ def device_args(work, device="cuda"):
 
 
 def algorithmic_bytes(work):
-    """One read of every logit row plus parameters and outputs."""
+    """One read of every logit row (and proposal row and mask word) plus
+    parameters and outputs."""
     rows, vocab = work["rows"].shape
     elem = 2 if work.get("dtype") == "bfloat16" else 4
     requests = len(work["offsets"]) - 1
     k1 = work["ids"].shape[1] + 1
     params = requests * (5 * 8 + 2 * 8) + rows * 8 + (requests + 1) * 8 + work["ids"].size * 8
     outputs = requests * (k1 * 8 + 3 * 4)
-    return rows * vocab * elem + params + outputs
+    logits = rows * vocab * elem
+    if work.get("draft_logits") is not None:
+        logits += work["draft_logits"].size * elem
+    if work.get("allowed") is not None:
+        logits += rows * (-(-vocab // 32)) * 4
+    return logits + params + outputs
 
 
 class Events:
@@ -344,10 +377,11 @@ def time_cell(name, steps, warmup):
     stream = torch.cuda.current_stream()
     lib = capi.load()
     p, r, o = args["params"], args["rng"], args["out"]
-    abi = capi.from_tensors(args["target_logits"], args["cu_rows"], args["draft_ids"], None, p.temperature,
-                            p.top_k, p.top_p, p.min_p, p.draft_kind, r.seed, r.stream_id, r.positions, None,
-                            args["plan"].workspace, o.tokens, o.accepted_len, o.status, o.path_used,
-                            mode=0 if work["mode"] == "ratio" else 1, max_draft=args["plan"].max_draft)
+    abi = capi.from_tensors(args["target_logits"], args["cu_rows"], args["draft_ids"], args.get("draft_logits"),
+                            p.temperature, p.top_k, p.top_p, p.min_p, p.draft_kind, r.seed, r.stream_id,
+                            r.positions, args.get("mask"), args["plan"].workspace, o.tokens, o.accepted_len,
+                            o.status, o.path_used, mode=0 if work["mode"] == "ratio" else 1,
+                            max_draft=args["plan"].max_draft)
     requests = len(work["offsets"]) - 1
     ev = Events()
 
@@ -404,6 +438,7 @@ def time_cell(name, steps, warmup):
     nbytes = algorithmic_bytes(work)
     med = float(np.median(calls))
     main_avg = float(main.mean())
+    cold_med = float(np.median(cold))
     return dict(rows=int(work["rows"].shape[0]), requests=requests,
                 median_us=med, mean_us=float(calls.mean()), p10_us=float(np.percentile(calls, 10)),
                 p90_us=float(np.percentile(calls, 90)),
@@ -411,8 +446,9 @@ def time_cell(name, steps, warmup):
                 host_us_per_call_abi=host_abi, host_us_per_call_op=host_op,
                 es_main_avg_us=main_avg, es_main_median_us=float(np.median(main)),
                 es_finish_avg_us=float(finish.mean()), es_finish_median_us=float(np.median(finish)),
-                cold_median_us=float(np.median(cold)), cold_es_main_median_us=float(np.median(cold_main)),
+                cold_median_us=cold_med, cold_es_main_median_us=float(np.median(cold_main)),
                 bytes=int(nbytes), call_gbs=nbytes / (med * 1e-6) / 1e9,
+                cold_call_gbs=nbytes / (cold_med * 1e-6) / 1e9,
                 es_main_gbs=nbytes / (main_avg * 1e-6) / 1e9,
                 cold_es_main_gbs=nbytes / (float(np.median(cold_main)) * 1e-6) / 1e9,
                 fallbacks=int(fallbacks),
@@ -456,6 +492,18 @@ def measured_traffic(path=os.path.join(os.path.dirname(os.path.abspath(__file__)
     return None
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(budget_s=12.0):
     """The FP64 oracle, single-threaded, over the headline rows (cycling through
     them) until the budget is spent; scaled to one 128-request call."""
@@ -474,7 +522,8 @@ def cpu_baseline(budget_s=12.0):
     elapsed = time.perf_counter() - t0
     per_row = elapsed / done
     return dict(value=per_row * 128 * 1e6, unit="us/call (128 requests, from the sample's time per row)",
-                cores=1, kind="port",
+                cores=1, kind="port", cpu_model=cpu_model(), host_nproc=os.cpu_count(),
+                host_affinity=len(os.sched_getaffinity(0)),
                 sample=f"{done} rows of the 128-row headline batch, cycled ({elapsed:.1f} s), through "
                        f"oracle.verify_reference with per-token scalar Philox: the FP64 restatement of "
                        f"reference.py, single threaded")
@@ -485,9 +534,7 @@ def main():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=20)
-    parser.add_argument("--cells", default="128x1,64x5,128x1_bf16,64x5_bf16,128x1_T1,64x5_T1,128x1_T0.7_p0.9,"
-                                           "64x5_T0.7_p0.9",
-                        help=f"comma-separated cells of {', '.join(CELLS)}")
+    parser.add_argument("--cells", default=DEFAULT_CELLS, help=f"comma-separated cells of {', '.join(CELLS)}")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -527,10 +574,16 @@ def main():
                                                   for k, v in copy.items()},
                    "cells": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv)
                                  for kk, vv in v.items()} for k, v in cells.items()}},
-        "roofline": {"bound": "hbm", "kernel": "es_main (slice stream), 128x1 cell, warm, timed region",
-                     "achieved": round(head["es_main_gbs"], 1), "peak": HBM_PEAK / 1e9,
-                     "unit": "GB/s", "frac": round(head["es_main_gbs"] * 1e9 / HBM_PEAK, 4),
-                     "traffic": measured_traffic()},
+        "roofline": {"bound": "hbm",
+                     "kernel": "the whole call (es_main + es_finish), 128x1 cell, cold: each call after a 2 GiB "
+                               "read that evicts the 256 MB Infinity Cache, timed with HIP events on the call's stream",
+                     "achieved": round(head["cold_call_gbs"], 1), "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": round(head["cold_call_gbs"] * 1e9 / HBM_PEAK, 4),
+                     "traffic": measured_traffic(),
+                     "traffic_kernel": "es_main (FETCH_SIZE + WRITE_SIZE per launch)",
+                     "call_warm_frac": round(head["call_gbs"] * 1e9 / HBM_PEAK, 4),
+                     "es_main_warm_frac": round(head["es_main_gbs"] * 1e9 / HBM_PEAK, 4),
+                     "es_main_cold_frac": round(head["cold_es_main_gbs"] * 1e9 / HBM_PEAK, 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -3,8 +3,9 @@
 // Two kernels per call (es_launch), on the caller's stream:
 //
 //  es_main, rows x slices blocks of 256 threads, each one register tile of up
-//  to 16 x 4 logits per thread (several tiles, read group by group, when the
-//  vocabulary needs more than MAX_SLICES tiles): one pass over a slice of a
+//  to 16 x 4 logits per thread (es_wide replaces it, with slices of several
+//  tiles read group by group, when a row needs more than MAX_SLICES tiles;
+//  such calls store no list candidates): one pass over a slice of a
 //  row: validation (NaN/+inf anywhere), the valid count, the largest valid
 //  logit and, for rows a list can finish, every valid logit at or above a
 //  threshold chosen so that the slice's top L are stored, or exactly its first
@@ -2195,16 +2196,27 @@ __device__ __forceinline__ void write_part(const es_arguments& a, int64_t row, i
   slice_parts(a, row)[slice] = part;
 }
 
-// A slice of several register tiles (a vocabulary past MAX_SLICES tiles):
-// the statistics over the slice read group by group (NaN/+inf anywhere, the
-// valid count, the maximum with its lowest ID) and the streaming draw. Such
-// calls store no list candidates (the host runs them with list_max 0), so
-// filtered rows take the full-row path.
+// es_wide, the slice pass of a call whose rows need more than MAX_SLICES
+// register tiles (launched in place of es_main): each slice of several tiles
+// is read group by group for the statistics (NaN/+inf anywhere, the valid
+// count, the maximum with its lowest ID) and the streaming draw. Such calls
+// store no list candidates (the host runs them with list_max 0), so filtered
+// rows take the full-row path.
 template <int DT, bool VEC>
-__device__ __noinline__ void wide_slice(const es_arguments& a, const Plan& pl, int64_t row, int slice, int64_t x0,
-                                        int64_t x1, Shared<typename Ty<DT>::W>& sh) {
+__global__ void __launch_bounds__(BLOCK) es_wide(es_arguments, Plan) {
   using W = typename Ty<DT>::W;
+  __shared__ Shared<W> sh;
+  const es_arguments& a = kernel_args().a;
+  const Plan pl = kernel_args().pl;
   const int tid = threadIdx.x, lane = lane_id();
+  if (blockIdx.x == 0 && tid == 0) reinterpret_cast<uint32_t*>(a.workspace)[1] = 0;  // the FP64 recompute count
+  const int64_t row = int(blockIdx.x) / pl.slices;
+  const int slice = int(blockIdx.x) - int(row) * pl.slices;
+  int64_t x0 = 0, x1 = 0;
+  if (tid < a.requests) {
+    x0 = at(a.cu_rows, tid);
+    x1 = at(a.cu_rows, tid + 1);
+  }
   Params p;
   slice_params(a, row, slice, x0, x1, &p, sh);
   if (p.status != ES_OK) return;
@@ -2300,10 +2312,6 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(5)))
   if (tid < a.requests) {
     x0 = at(a.cu_rows, tid);
     x1 = at(a.cu_rows, tid + 1);
-  }
-  if (pl.tiles > 1) {
-    wide_slice<DT, VEC>(a, pl, row, slice, x0, x1, sh);
-    return;
   }
   __builtin_amdgcn_sched_barrier(0);
   // Tile loads. Groups past the slice's end are loaded as copies of its last
@@ -2905,9 +2913,10 @@ hipError_t launch_main(const es_arguments& a, const Plan& pl, hipStream_t stream
   // es_main: the slice blocks; es_finish: one block per row, then the
   // request blocks.
   hipError_t err = hipSuccess;
+  const void* slice_kernel = pl.tiles > 1 ? reinterpret_cast<const void*>(&es_wide<DT, VEC>)
+                                          : reinterpret_cast<const void*>(&es_main<DT, VEC, G>);
   if (a.rows > 0)
-    err = hipLaunchKernel(reinterpret_cast<const void*>(&es_main<DT, VEC, G>), dim3(unsigned(pl.slice_blocks)),
-                          dim3(BLOCK), params, 0, stream);
+    err = hipLaunchKernel(slice_kernel, dim3(unsigned(pl.slice_blocks)), dim3(BLOCK), params, 0, stream);
   if (err == hipSuccess && split) err = hipEventRecord(split, stream);
   if (err != hipSuccess) return err;
   return hipLaunchKernel(reinterpret_cast<const void*>(&es_finish<DT, VEC>),

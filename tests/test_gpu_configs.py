@@ -1,9 +1,15 @@
-"""GPU parity at the benchmark's shapes (V = 151,936, 128 and 320 rows).
+"""GPU parity at the benchmark's configurations (V = 151,936).
 
-Rows of this vocabulary take ten slices of the 16-group register tile, the
-geometry the benchmark measures. Each is checked token-for-token against the FP64 oracle, and the
-list finish must settle every row without an FP64 fallback.
+Every configuration is checked token for token against the FP64 oracle: the
+128-request and 64 x 5 cells (every row must finish as a top-k list without
+an FP64 fallback), temperature-only rows, the flatness configuration's top-p
+and min-p rows in batches of 128 and 1, and the full ragged verification
+configuration (256 requests, against its committed oracle outputs, and
+under two other slot orders).
 """
+import os
+import sys
+
 import numpy as np
 import pytest
 
@@ -197,3 +203,89 @@ def test_ragged_masked_mixed_filters(variant):
     """24 requests of the ragged configuration: draft lengths 0..7, a mask
     allowing 10% of each row, mixed filters, permuted slots."""
     _run(bench.config5(requests=24, variant=variant))
+
+
+# ---- The full ragged configuration: 256 requests, about 1,150 rows. ----
+# Expected outputs: tests/golden/config5_outputs.npz, written by the FP64
+# oracle with tests/golden/make_config5_golden.py, with the sha256 of every
+# input. The three variants share their inputs; only the draft kind, the mode
+# and the proposal logits differ.
+
+CONFIG5_GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config5_outputs.npz")
+
+
+@pytest.fixture(scope="module")
+def config5_full():
+    return bench.config5(requests=256, variant="full_ratio")
+
+
+def _variant(work, variant):
+    out = dict(work)
+    n = len(work["offsets"]) - 1
+    out["params"] = dict(work["params"], draft_kind=["one_hot" if variant == "one_hot_coupled" else "full"] * n)
+    out["mode"] = "ratio" if variant == "full_ratio" else "coupled"
+    out["draft_logits"] = None if variant == "one_hot_coupled" else work["draft_logits"]
+    return out
+
+
+def _permuted(work, order):
+    """The same requests in slots `order` (slot s holds request order[s])."""
+    offsets = work["offsets"]
+    spans = [np.arange(offsets[r], offsets[r + 1]) for r in order]
+    rows = np.concatenate(spans)
+    sizes = [len(s) for s in spans]
+    out = dict(work)
+    out["rows"] = work["rows"][rows]
+    out["allowed"] = work["allowed"][rows]
+    if work["draft_logits"] is not None:
+        out["draft_logits"] = work["draft_logits"][rows]
+    out["offsets"] = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    out["ids"] = work["ids"][order]
+    out["keys"] = dict(seed=work["keys"]["seed"][order], stream=work["keys"]["stream"][order],
+                       positions=work["keys"]["positions"][rows])
+    out["params"] = {k: (list(np.asarray(v, dtype=object)[order]) if isinstance(v, list) else v)
+                     for k, v in work["params"].items()}
+    return out
+
+
+def _device_outputs(work):
+    from exactsample.cuda import verify
+    args = bench.device_args(work)
+    out = verify(**args, mode=work["mode"])
+    args["plan"].synchronize()
+    n = len(work["offsets"]) - 1
+    return {f: getattr(out, f).cpu().numpy()[:n] for f in ("tokens", "accepted_len", "status", "path_used")}
+
+
+@pytest.mark.parametrize("variant", ["full_ratio", "one_hot_coupled", "full_coupled"])
+def test_full_ragged_configuration(config5_full, variant):
+    import hashlib
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+    from make_config5_golden import input_digests
+    golden = np.load(CONFIG5_GOLDEN)
+    work = _variant(config5_full, variant)
+    for name, value in input_digests(work).items():
+        assert str(golden[f"{variant}/sha256/{name}"]) == value, f"input {name} differs from the golden batch's"
+    got = _device_outputs(work)
+    for field in ("tokens", "accepted_len", "status"):
+        np.testing.assert_array_equal(got[field], golden[f"{variant}/{field}"], err_msg=field)
+    assert (got["path_used"] == 1).all()
+    if variant != "full_ratio":
+        return
+    # Batch invariance: the same requests in two other slot orders give
+    # byte-identical per-request outputs.
+    n = len(work["offsets"]) - 1
+    for seed in (1, 2):
+        order = np.random.default_rng(seed).permutation(n)
+        moved = _device_outputs(_permuted(work, order))
+        for field in ("tokens", "accepted_len", "status", "path_used"):
+            assert hashlib.sha256(moved[field].tobytes()).digest() == hashlib.sha256(
+                got[field][order].tobytes()).digest(), field
+
+
+# ---- Top-p and min-p at batch 1: single rows of the flatness configuration. ----
+@pytest.mark.parametrize("filt", ["top_p", "min_p"])
+@pytest.mark.parametrize("row", [0, 1, 7, 10, 33, 90])
+def test_flatness_rows_one_at_a_time(filt, row):
+    """Rows 0, 10 and 90 are the constructed ones (a threshold within an ulp)."""
+    _run(bench.config3_single(filt=filt, row=row))
