@@ -52,6 +52,15 @@ constexpr int TOPP_SLICE_NEED = 64;       // candidates per slice for a top-p li
 constexpr int LIST_LIMIT = 1024;          // largest candidate union the merge takes
 constexpr int HEAD_BINS = 256;            // quarter-logit bins below the maximum for the union's head
 constexpr int TOPP_HEAD = 96;             // entries a top-p list sorts first
+// Binned top-p rows: each slice bins its kept tokens on the grid y = l * 4 / T
+// (bin b holds y in [b, b + 1), a quarter of a unit of x = (l - max) / T), in
+// the 64 bins below its reference maximum: per bin the count and the sum of
+// e^((y - b - 1/2) / 4), i.e. the weights relative to the bin's centre. The
+// grid is absolute, so the slices' bins merge by addition.
+constexpr int TP_COARSE = 64;
+constexpr double TP_Y_PER_X = 4.0;
+constexpr size_t TP_SLICE_BIN_BYTES = TP_COARSE * (sizeof(double) + sizeof(uint16_t));
+constexpr int TP_SLICES_MAX = int(CAND_BYTES / TP_SLICE_BIN_BYTES);
 
 // ---------------------------------------------------------------------------
 // Element types.
@@ -145,6 +154,14 @@ template <class W> __device__ __forceinline__ Cand<W>* candidates(const es_argum
 struct Pick;
 template <class W> __device__ __forceinline__ Pick* slice_pick(const es_arguments& a, int64_t row, int slice, int cap) {
   return reinterpret_cast<Pick*>(candidates<W>(a, row) + int64_t(slice) * cap);
+}
+// A binned top-p row's slice keeps its bins where a list row keeps candidates:
+// TP_COARSE FP64 masses, then TP_COARSE 16-bit counts.
+__device__ __forceinline__ double* slice_bin_mass(const es_arguments& a, int64_t row, int slice) {
+  return reinterpret_cast<double*>(row_region(a, row) + OFF_CAND + size_t(slice) * TP_SLICE_BIN_BYTES);
+}
+__device__ __forceinline__ uint16_t* slice_bin_count(const es_arguments& a, int64_t row, int slice) {
+  return reinterpret_cast<uint16_t*>(slice_bin_mass(a, row, slice) + TP_COARSE);
 }
 
 // ---------------------------------------------------------------------------
@@ -520,11 +537,14 @@ struct ListPlan {
   int need, L;
   bool sorted_list;  // a top-k row (k <= 64, within the slice capacity) finished by one wave
   bool need_topp;    // a top-p list: the slices also sum their kept weights
+  bool binned;       // a top-p row without a top-k cut or min-p: the slices bin their kept weights
 };
-__device__ __forceinline__ ListPlan list_plan(const Params& p, int list_max, int cap, int64_t vocab) {
-  ListPlan lp{0, 0, false, false};
+__device__ __forceinline__ ListPlan list_plan(const Params& p, int list_max, int cap, int64_t vocab, int slices) {
+  ListPlan lp{0, 0, false, false, false};
   if (p.temperature > 0 && list_max > 0 && !p.full_q && !stream_row(p, vocab)) {
     if (p.top_k >= 1 && p.top_k <= list_max) lp.need = int(p.top_k);
+    else if (p.top_p < 1 && p.min_p == 0 && (p.top_k == 0 || p.top_k >= vocab) && slices <= TP_SLICES_MAX)
+      lp.binned = true;
     else if (p.top_p < 1 && p.min_p == 0) lp.need = TOPP_SLICE_NEED;
     else lp.need = -1;
   }
@@ -1186,6 +1206,194 @@ __device__ __forceinline__ int wave_topk(const es_arguments& a, int64_t row, con
 }
 
 // ---------------------------------------------------------------------------
+// The streaming draw of stream rows (reference: fused.cuh:532-681 row_scan and
+// its Pick merge :301-314).
+template <class SH> __device__ __forceinline__ Pick block_pick(Pick pk, SH& sh) {
+  pk = wave_all(pk, pick_join, pick_none());
+  __syncthreads();
+  if (lane_id() == 0) sh.picks[wave_id()] = pk;
+  __syncthreads();
+  Pick r = sh.picks[0];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) r = pick_join(r, sh.picks[w]);
+  __syncthreads();
+  return r;
+}
+
+// A thread's Kahan sum of exp(x) over kept tokens with x >= SUM_PRUNE, its
+// error bound term, and the count of kept tokens below SUM_PRUNE.
+struct KahanSum {
+  float s = 0.f, c = 0.f, e = 0.f;
+  int pruned = 0;
+  float pruned_max = -INFINITY;  // the largest x left out
+  __device__ __forceinline__ void add(float x) {
+    if (!(x >= SUM_PRUNE)) {
+      ++pruned;
+      pruned_max = fmaxf(pruned_max, x);
+      return;
+    }
+    const float w = weight32(x), d = w - c, t = s + d;
+    c = (t - s) - d;
+    s = t;
+    e += w * (X_ERR * (1.f + fabsf(x)));
+  }
+};
+
+// One group of four tokens into a thread's certified pick: tokens whose bit
+// is set in `bits`, above -inf, not `excluded` and passing keep(v, x), scored
+// x + G(word(sub, t)) with x = tp.x32(v). A token whose score bound stays
+// under `bar` (the floor, then the thread's best lower bound) needs no Philox
+// word; one Philox call serves the group's four tokens. With SUM, every such
+// token (the excluded one too) also goes into `sum`.
+template <bool SUM, class W, class Keep>
+__device__ __forceinline__ void pick_group(int g, const W (&x)[4], uint32_t bits, const Temp<W>& tp,
+                                           const RngAddr& rng, uint32_t sub, int excluded, Keep&& keep, Pick& best,
+                                           float& bar, KahanSum* sum) {
+  float xs[4];
+  uint32_t live = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const W v = x[j];
+    xs[j] = tp.x32(v);
+    const bool ok = ((bits >> j) & 1u) && v > neg_inf<W>() && keep(v, xs[j]);
+    if constexpr (SUM) {
+      if (ok) sum->add(xs[j]);
+    }
+    if (!ok || 4 * g + j == excluded) continue;
+    const float ub = xs[j] + GUMBEL_MAX + SCORE_ERR * (1.f + fabsf(xs[j]) + GUMBEL_MAX);
+    if (ub < bar) {
+      best.others = fmaxf(best.others, ub);
+      continue;
+    }
+    live |= 1u << j;
+  }
+  if (!live) return;
+  const Words w4 = philox(rng.seed, rng.stream, rng.position, sub, uint32_t(g));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (!((live >> j) & 1u)) continue;
+    const uint32_t w = w4.w[j];
+    const float gb = gumbel_upper(w);
+    const float ub2 = xs[j] + gb + SCORE_ERR * (1.f + fabsf(xs[j]) + fabsf(gb));
+    if (ub2 < bar) {
+      best.others = fmaxf(best.others, ub2);
+      continue;
+    }
+    const float G = gumbel32(w), sc = xs[j] + G, e = SCORE_ERR * (1.f + fabsf(xs[j]) + fabsf(G));
+    const int t = 4 * g + j;
+    if (sc > best.mid || (sc == best.mid && t < best.id)) {
+      best.others = fmaxf(best.others, best.hi);
+      best = Pick{sc, sc - e, sc + e, best.others, t};
+    } else {
+      best.others = fmaxf(best.others, sc + e);
+    }
+    bar = fmaxf(bar, best.lo - PRUNE_MARGIN);
+  }
+}
+
+// The thread's certified pick over the allowed tokens of groups [g_begin,
+// g_end) read from memory, B groups in flight per thread (thread k takes
+// g_begin + k, + BLOCK, ...).
+template <int B, bool SUM, int DT, bool VEC, class Keep>
+__device__ __forceinline__ Pick range_pick(const es_arguments& a, int64_t row, const RowView<DT, VEC>& view,
+                                           int g_begin, int g_end, const Temp<typename Ty<DT>::W>& tp,
+                                           const RngAddr& rng, uint32_t sub, int excluded, float floor, Keep&& keep,
+                                           KahanSum* sum) {
+  using W = typename Ty<DT>::W;
+  Pick best = pick_none();
+  float bar = floor - PRUNE_MARGIN;
+  // Every lane runs the same number of rounds (groups past the range carry no
+  // tokens), so after each round the wave can share its best lower bound: a
+  // token whose upper bound stays below it cannot win, and is kept only as a
+  // loser's bound, as with the thread's own best.
+  for (int base0 = g_begin; base0 < g_end; base0 += B * BLOCK) {
+    const int base = base0 + int(threadIdx.x);
+    W x[B][4];
+    uint32_t mb[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int g = base + u * BLOCK;
+      view.load(min(g, g_end - 1), x[u]);
+      mb[u] = g < g_end ? group_bits(a, row, g) : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u) pick_group<SUM>(base + u * BLOCK, x[u], mb[u], tp, rng, sub, excluded, keep, best, bar, sum);
+    const float wave_lo = wave_all(best.lo, [](float p, float q) { return p > q ? p : q; }, -INFINITY);
+    bar = fmaxf(bar, wave_lo - PRUNE_MARGIN);
+  }
+  return best;
+}
+
+// ---------------------------------------------------------------------------
+// The full-row path's binned top-p boundary works on bins of the absolute
+// grid y = l * 4 / T (see slice_bins): bin b = floor(y) holds a run of
+// consecutive tokens of the (logit desc, ID asc) order, since floor(l * 4 / T)
+// is monotone in l. A dense boundary bin is split 64 ways on the finer grid
+// floor(64 y), which nests in it.
+constexpr int TP_BINS = 1024;  // fine bins of the boundary's coarse range, at most
+constexpr int TP_SCALARS = 16;
+
+// e^d for |d| <= 1/8: the Taylor polynomial through d^11 (truncation below
+// 3e-18 relative), in FP64 with explicit fused multiply-adds.
+__device__ __forceinline__ double exp_center(double d) {
+  double r = 1.0 / 39916800.0;
+  r = fma(r, d, 1.0 / 3628800.0);
+  r = fma(r, d, 1.0 / 362880.0);
+  r = fma(r, d, 1.0 / 40320.0);
+  r = fma(r, d, 1.0 / 5040.0);
+  r = fma(r, d, 1.0 / 720.0);
+  r = fma(r, d, 1.0 / 120.0);
+  r = fma(r, d, 1.0 / 24.0);
+  r = fma(r, d, 1.0 / 6.0);
+  r = fma(r, d, 0.5);
+  r = fma(r, d, 1.0);
+  return fma(r, d, 1.0);
+}
+
+// e^d for |d| <= 1/64 + tiny: the Taylor polynomial through d^7 (truncation
+// below 2e-17), in FP64 with explicit fused multiply-adds.
+__device__ __forceinline__ double exp_near_zero(double d) {
+  double r = 1.0 / 5040.0;
+  r = fma(r, d, 1.0 / 720.0);
+  r = fma(r, d, 1.0 / 120.0);
+  r = fma(r, d, 1.0 / 24.0);
+  r = fma(r, d, 1.0 / 6.0);
+  r = fma(r, d, 0.5);
+  r = fma(r, d, 1.0);
+  return fma(r, d, 1.0);
+}
+
+// The row's bins (es_finish only; the gathered tokens of the boundary bins
+// live in the block's list union).
+struct TopPBins {
+  double mass[TP_BINS];   // sum over the bin's kept tokens of their weights relative to the bin's centre
+  unsigned cnt[TP_BINS];  // kept tokens in the bin
+  double scal[TP_SCALARS];
+  int n;                  // tokens gathered
+};
+
+// Sorts keys[0, n) descending in the block (bitonic, n a power of two >= 64;
+// every thread calls it).
+template <class K> __device__ __forceinline__ void block_sort_desc(K* keys, int n) {
+  for (int size = 2; size <= n; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      __syncthreads();
+      for (int i = threadIdx.x; i < (n >> 1); i += BLOCK) {
+        const int lo = 2 * i - (i & (stride - 1));  // the pair (lo, lo + stride)
+        const int hi = lo + stride;
+        const bool desc = (lo & size) == 0;          // this run sorts descending
+        const K x = keys[lo], y = keys[hi];
+        if ((x < y) == desc) {
+          keys[lo] = y;
+          keys[hi] = x;
+        }
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
 // Full-row path: one block re-reads the row (and the proposal row) as often as
 // it needs. Exact integer cuts, exact (certified or superaccumulated) FP64
 // sums, certified FP32 draws with FP64 rescoring.
@@ -1201,9 +1409,12 @@ template <int DT, bool VEC> struct FullRow {
   Temp<W> tp;
   int fallbacks;
 
-  __device__ __forceinline__ FullRow(const es_arguments& a_, int64_t row_, const Params& p_, Shared<W>& sh_, int groups_)
+  TopPBins* tb;  // the binned top-p boundary's storage, or null
+
+  __device__ __forceinline__ FullRow(const es_arguments& a_, int64_t row_, const Params& p_, Shared<W>& sh_, int groups_,
+                                     TopPBins* tb_ = nullptr)
       : a(a_), row(row_), p(p_), sh(sh_), view(a_.target, row_, int(a_.vocab)), qview(a_.draft, row_, int(a_.vocab)),
-        groups(groups_), fallbacks(0) {}
+        groups(groups_), fallbacks(0), tb(tb_) {}
 
   // Calls f(t, v, allowed) for every token of the row (or of the proposal row).
   template <bool Q, class F> __device__ __forceinline__ void each(F&& f) const {
@@ -1467,6 +1678,471 @@ template <int DT, bool VEC> struct FullRow {
     return prefix;
   }
 
+  // ---- The binned top-p boundary ----
+  // The top-p cut of a row whose slices binned its kept weights (TP_COARSE
+  // bins of a quarter unit of x on the absolute grid y = l * 4 / T, see
+  // slice_bins), in one pass over the row, two when the boundary's bins are
+  // dense:
+  //  1. the slices' bins merge into the row's 64 bins below the maximum; from
+  //     certified prefix bounds against top_p times the total they give the
+  //     bins [b_lo, b_hi] that may hold the boundary (reference.py:73-83);
+  //  2. one pass gathers the tokens of [b_lo, b_hi] into the block's list
+  //     (or, past GATHER_CAP of them, bins them again 64 times finer and a
+  //     second pass gathers the fine bins that may hold the boundary), and
+  //     takes the certified FP32 Gumbel-max of draw `sub` (draft `excluded`
+  //     left out) over the tokens before them, which are certainly kept; an
+  //     FP32 screen settles most tokens with one compare;
+  //  3. the gathered tokens are sorted (logit desc, ID asc) with their FP64
+  //     weights (the oracle's formula); the boundary is the first whose
+  //     double-double prefix sum plus the mass before them certainly reaches
+  //     the target. The total is refined with the gathered weights' exact
+  //     sum; an uncertain boundary with nothing before the gathered tokens is
+  //     settled with exact prefix sums.
+  // The draw's pick over the gathered part of the nucleus joins the pick of
+  // the tokens before it. Returns false, changing nothing the caller relies
+  // on, when the bins cannot settle the row (the boundary below the binned
+  // range, too many tokens in its bins, an uncertain boundary after the first
+  // bin, a grid out of range); the caller then takes mass_boundary.
+  struct BinnedCut {
+    u128 cut;               // keep composite keys >= cut
+    double den_lo, den_hi;  // the nucleus mass (the rounded prefix through the cut) lies in [den_lo, den_hi]
+    bool den_exact;         // den_lo == den_hi is the correctly rounded value
+    Pick pick;              // certified pick of draw `sub` over the nucleus
+  };
+  using GKey = typename std::conditional<sizeof(W) == 4, uint64_t, u128>::type;
+  static constexpr int GATHER_CAP = 1024;
+  static constexpr int FINE_PER_COARSE = 64;  // fine bins: y * 64 on the same grid
+  static_assert(GATHER_CAP * (sizeof(GKey) + sizeof(double)) <= sizeof(Shared<W>::u), "gathered tokens fit the union");
+
+  __device__ __forceinline__ GKey gkey(W v, int t) const { return GKey(CK<W>::make(v, t)); }
+  __device__ __forceinline__ W gvalue(GKey k) const { return CK<W>::value(u128(k)); }
+  __device__ __forceinline__ int gid(GKey k) const { return ck_id(u128(k)); }
+
+  // One pass over the row, TG groups of four in flight per thread and one
+  // group processed at a time (the loaded groups rotate through a fixed
+  // register slot, keeping the loop body to one copy): f(g, x, bits) per
+  // group, then round() once per round, in every lane.
+  template <class F, class R> __device__ __forceinline__ void each_group(F&& f, R&& round) const {
+    for (int base0 = 0; base0 < groups; base0 += BLOCK * TG) {
+      const int base = base0 + int(threadIdx.x);
+      W x[TG][4];
+      uint32_t bits[TG];
+#pragma unroll
+      for (int u = 0; u < TG; ++u) {
+        const int g = base + u * BLOCK;
+        if (g < groups) {
+          view.load(g, x[u]);
+          bits[u] = group_bits(a, row, g);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) x[u][j] = neg_inf<W>();
+          bits[u] = 0;
+        }
+      }
+#pragma unroll 1
+      for (int u = 0; u < TG; ++u) {
+        f(base + u * BLOCK, x[0], bits[0]);
+#pragma unroll
+        for (int q = 0; q + 1 < TG; ++q) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) x[q][j] = x[q + 1][j];
+          bits[q] = bits[q + 1];
+        }
+      }
+      round();
+    }
+  }
+
+  int bin_slices = 0;  // > 0: the row's slices binned its kept weights
+
+  __device__ __forceinline__ bool topp_binned(uint32_t sub, int excluded, int floor_id, BinnedCut* out) {
+    if (!bin_slices || !tb || tp.slow) return false;
+    TopPBins& b = *tb;
+    const int tid = threadIdx.x, lane = lane_id(), wid = wave_id();
+    const double inv_t = 1.0 / p.temperature, inv4 = TP_Y_PER_X / p.temperature;
+    const double M = tp.M, yM = M * inv4;
+    if (!(fabs(yM) < 0x1p50)) return false;
+    const double top = floor(yM), dM = top - yM;  // dM in (-1, 0]
+    // A mass's relative error besides its adds: the polynomial, y's formation
+    // (|y| 2^-53 per token and for dM) and the FP64 exp of the bin factor.
+    const double rel = 1e-14 + fabs(yM) * 0x1p-50;
+    auto coarse_of = [&](W v) -> double { return top - floor(double(v) * inv4); };
+    // The x of the lower edge of row bin k (bin top - k holds y in [top - k, top - k + 1)).
+    auto coarse_edge = [&](double k) -> float { return float((dM - k) * (1.0 / TP_Y_PER_X)); };
+    // ---- 1. The row's bins. ----
+    if (tid < TP_COARSE) { b.mass[tid] = 0; b.cnt[tid] = 0; }
+    if (tid == 0) b.n = 0;
+    __syncthreads();
+    double fp = 0, fpe = 0;  // mass past the row's bins and its bound (FP64)
+    for (int idx = tid; idx < bin_slices * TP_COARSE; idx += BLOCK) {
+      const int sl = idx / TP_COARSE, j = idx - sl * TP_COARSE;
+      const unsigned c = slice_bin_count(a, row, sl)[j];
+      if (!c) continue;
+      const double m = slice_bin_mass(a, row, sl)[j];
+      const double k = double(j) + (top - slice_parts(a, row)[sl].frontier);
+      if (k < double(TP_COARSE)) {
+        atomicAdd(&b.mass[int(k)], m);
+        atomicAdd(&b.cnt[int(k)], c);
+      } else {
+        const double f = exp((dM + 0.5 - k) * (1.0 / TP_Y_PER_X)) * m;
+        fp += f;
+        fpe += f * (rel + double(c) * 0x1p-52);
+      }
+    }
+    if (tid < bin_slices) {  // the slices' FP32 far parts, from their reference maximum to the row's
+      const SlicePart q = slice_parts(a, row)[tid];
+      const double sh_x = (q.tau - M) * inv_t;
+      const double sc = exp(sh_x);
+      fp += q.sum * sc;
+      fpe += (q.err + 1e-15 * q.sum) * sc * (1 + 1e-13) + q.sum * sc * (fabs(sh_x) * 0x1p-50 + 1e-15);
+    }
+    const double fp_all = block_all(fp, [](double x, double y) { return x + y; }, sh.dred, 0.0);
+    const double fpe_all = block_all(fpe, [](double x, double y) { return x + y; }, sh.dred, 0.0) + 0x1p-44 * fp_all;
+    // One wave: lane k holds row bin k. Certified inclusive prefix sums, the
+    // bins that may hold the boundary and the mass outside them.
+    if (wid == 0) {
+      const double f = exp((dM + 0.5 - double(lane)) * (1.0 / TP_Y_PER_X));
+      const double m = f * b.mass[lane];
+      const double e = m * (rel + double(b.cnt[lane]) * 0x1p-52);
+      struct ME { double m, e; };
+      const ME inc = wave_scan(ME{m, e}, [](ME x, ME y) { return ME{x.m + y.m, x.e + y.e}; }, ME{0, 0});
+      const ME tot = lane_read(inc, WAVE - 1);
+      const double slack = inc.e + 0x1p-44 * inc.m, tslack = tot.e + 0x1p-44 * tot.m;
+      const double s_lo = tot.m - tslack + fp_all - fpe_all, s_hi = tot.m + tslack + fp_all + fpe_all;
+      const double lo_t = p.top_p * s_lo * (1 - 0x1p-50), hi_t = p.top_p * s_hi * (1 + 0x1p-50);
+      const uint64_t may = __ballot(inc.m + slack >= lo_t * (1 - 0x1p-50));
+      const uint64_t sure = __ballot(inc.m - slack >= hi_t);
+      const int b_lo = may ? __ffsll((unsigned long long)may) - 1 : TP_COARSE;
+      const int b_hi = sure ? __ffsll((unsigned long long)sure) - 1 : TP_COARSE;
+      const int count = wave_all(lane >= b_lo && lane <= b_hi ? int(b.cnt[lane]) : 0, [](int x, int y) { return x + y; }, 0);
+      // Mass before b_lo and after b_hi (inside the bins), each with its bound.
+      const ME before = wave_all(lane < b_lo ? ME{m, e} : ME{0, 0}, [](ME x, ME y) { return ME{x.m + y.m, x.e + y.e}; }, ME{0, 0});
+      const ME after = wave_all(lane > b_hi ? ME{m, e} : ME{0, 0}, [](ME x, ME y) { return ME{x.m + y.m, x.e + y.e}; }, ME{0, 0});
+      if (lane == 0) {
+        b.scal[0] = b_lo; b.scal[1] = b_hi; b.scal[2] = count;
+        b.scal[3] = lo_t; b.scal[4] = hi_t;
+        const double be = before.e + 0x1p-44 * before.m, ae = after.e + 0x1p-44 * after.m;
+        b.scal[5] = fmax(before.m - be, 0.0); b.scal[6] = before.m + be;
+        // Everything outside [b_lo, b_hi]: the bins before and after, and the far tail.
+        b.scal[7] = fmax(before.m - be + after.m - ae + fp_all - fpe_all, 0.0);
+        b.scal[8] = before.m + be + after.m + ae + fp_all + fpe_all;
+      }
+    }
+    __syncthreads();
+    const int b_lo = int(b.scal[0]), b_hi = int(b.scal[1]), count = int(b.scal[2]);
+    double lo_t = b.scal[3], hi_t = b.scal[4];
+    double eb_lo = b.scal[5], eb_hi = b.scal[6];
+    const double rest_lo = b.scal[7], rest_hi = b.scal[8];
+    __syncthreads();
+    if (b_hi >= TP_COARSE || b_lo > b_hi || count == 0) return false;  // the boundary may lie in the far tail
+    // ---- 2. Gather the boundary's tokens; pick over the ones before them. ----
+    GKey* keys = reinterpret_cast<GKey*>(&sh.u);
+    double* wts = reinterpret_cast<double*>(keys + GATHER_CAP);
+    const float edge_before = coarse_edge(double(b_lo) - 1.0);  // x at or above it: coarse bin < b_lo
+    const float edge_range = coarse_edge(double(b_hi));          // x below it: coarse bin > b_hi
+    constexpr float SCREEN = 1e-5f;  // above x32's error for |x| <= 17
+    // Tokens before the gathered range are certainly kept (their bin lies
+    // before the boundary's); the range's lower end in fine bins, if any.
+    double fine_top = 0;  // fine index of a token: fine_top - floor(y * 64)
+    int f_lo = -1;        // >= 0: gather fine bins [f_lo, f_hi] of the coarse range
+    int f_hi = -1;
+    auto before_range = [&](W v, float x) -> bool {
+      if (x < edge_before - SCREEN) {
+        if (f_lo < 0 || x < edge_range - SCREEN) return false;
+      } else if (x > edge_before + SCREEN) {
+        return true;
+      }
+      const double k = coarse_of(v);
+      if (k < double(b_lo)) return true;
+      if (f_lo < 0 || k > double(b_hi)) return false;
+      return fine_top - floor(double(v) * inv4 * FINE_PER_COARSE) < double(f_lo);
+    };
+    float floor_score = -INFINITY;
+    if (floor_id >= 0 && floor_id != excluded && b_lo > 0) {
+      const W v = view.value(floor_id);
+      const float x = tp.x32(v);
+      if (tp.kept(v, x) && coarse_of(v) < double(b_lo)) {
+        const float g = gumbel32(word_of(p.rng, sub, uint32_t(floor_id)));
+        floor_score = x + g - SCORE_ERR * (1.f + fabs(x) + fabsf(g));
+      }
+    }
+    Pick best = pick_none();
+    float bar = floor_score - PRUNE_MARGIN;
+    auto share_bar = [&]() {
+      bar = fmaxf(bar, wave_all(best.lo, [](float u, float v) { return u > v ? u : v; }, -INFINITY) - PRUNE_MARGIN);
+    };
+    auto keep_before = [&](W v, float x) { return tp.kept(v, x) && before_range(v, x); };
+    const bool dense = count > GATHER_CAP;
+    if (dense) {
+      // The coarse range binned 64 times finer (y * 64 on the same grid):
+      // fine bin f of coarse bin k is 64 k + (63 - (floor(64 y) - 64 floor(y))).
+      fine_top = (top + 1) * FINE_PER_COARSE - 1;
+      const int nfine = (b_hi - b_lo + 1) * FINE_PER_COARSE;
+      if (nfine > TP_BINS) return false;
+      for (int i = tid; i < nfine; i += BLOCK) { b.mass[i] = 0; b.cnt[i] = 0; }
+      __syncthreads();
+      const double base = double(b_lo) * FINE_PER_COARSE;
+      each_group([&](int g, const W (&x)[4], uint32_t bits) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const W v = x[j];
+          if (!(((bits >> j) & 1u) && v > neg_inf<W>())) continue;
+          const float x32 = tp.x32(v);
+          if (x32 < edge_range - SCREEN || x32 > edge_before + SCREEN) continue;
+          const double k = coarse_of(v);
+          if (k < double(b_lo) || k > double(b_hi) || !tp.kept(v, x32)) continue;
+          const double fy = double(v) * inv4 * FINE_PER_COARSE, fb = floor(fy);
+          const int i = int(fine_top - fb - base);  // in [0, nfine): the fine grid nests in the coarse one
+          if (i < 0 || i >= nfine) continue;
+          atomicAdd(&b.mass[i], exp_near_zero((fy - fb - 0.5) * (1.0 / (TP_Y_PER_X * FINE_PER_COARSE))));
+          atomicAdd(&b.cnt[i], 1u);
+        }
+        if (b_lo > 0) pick_group<false>(g, x, bits, tp, p.rng, sub, excluded, keep_before, best, bar, nullptr);
+      }, share_bar);
+      __syncthreads();
+      // The fine prefix, after the mass before the coarse range, in thread order.
+      const double fdM = (dM + 1.0) * (1.0 / TP_Y_PER_X);
+      double fm = 0, fe = 0;
+      constexpr int PF = TP_BINS / BLOCK;
+      double mm[PF], ee[PF];
+#pragma unroll
+      for (int q = 0; q < PF; ++q) {
+        const int i = PF * tid + q;
+        mm[q] = 0; ee[q] = 0;
+        if (i < nfine) {
+          const double fidx = base + double(i);
+          mm[q] = exp(fdM - (fidx + 0.5) * (1.0 / (TP_Y_PER_X * FINE_PER_COARSE))) * b.mass[i];
+          ee[q] = mm[q] * (rel + double(b.cnt[i]) * 0x1p-52);
+        }
+        fm += mm[q]; fe += ee[q];
+      }
+      struct ME { double m, e; };
+      const ME inc = wave_scan(ME{fm, fe}, [](ME x, ME y) { return ME{x.m + y.m, x.e + y.e}; }, ME{0, 0});
+      __syncthreads();
+      if (lane == WAVE - 1) { b.scal[8 + wid] = inc.m; b.scal[12 + wid] = inc.e; }
+      __syncthreads();
+      double rm = (eb_lo + eb_hi) * 0.5, re = (eb_hi - eb_lo) * 0.5;
+      for (int w = 0; w < wid; ++w) { rm += b.scal[8 + w]; re += b.scal[12 + w]; }
+      rm += inc.m - fm;
+      re += inc.e - fe;
+      int flo = INT_MAX, fhi = INT_MAX, fcount = 0;
+      double feb_lo = 0, feb_hi = 0;
+      bool have_before = false;
+#pragma unroll
+      for (int q = 0; q < PF; ++q) {
+        const int i = PF * tid + q;
+        rm += mm[q]; re += ee[q];
+        if (i >= nfine) continue;
+        const double sl = re + 0x1p-44 * rm;
+        if (rm + sl >= lo_t * (1 - 0x1p-50)) flo = min(flo, i);
+        if (rm - sl >= hi_t) fhi = min(fhi, i);
+      }
+      auto mn = [](int x, int y) { return x < y ? x : y; };
+      f_lo = block_all(flo, mn, sh.ired, INT_MAX);
+      f_hi = block_all(fhi, mn, sh.ired, INT_MAX);
+      if (f_hi == INT_MAX || f_lo > f_hi) return false;
+      // The mass before fine bin f_lo and the count of [f_lo, f_hi].
+      rm = (eb_lo + eb_hi) * 0.5; re = (eb_hi - eb_lo) * 0.5;
+      for (int w = 0; w < wid; ++w) { rm += b.scal[8 + w]; re += b.scal[12 + w]; }
+      rm += inc.m - fm;
+      re += inc.e - fe;
+#pragma unroll
+      for (int q = 0; q < PF; ++q) {
+        const int i = PF * tid + q;
+        if (i == f_lo) { const double sl = re + 0x1p-44 * rm; feb_lo = rm - sl; feb_hi = rm + sl; have_before = true; }
+        rm += mm[q]; re += ee[q];
+        if (i >= f_lo && i <= f_hi && i < nfine) fcount += int(b.cnt[i]);
+      }
+      __syncthreads();
+      if (have_before) { b.scal[5] = fmax(feb_lo, 0.0); b.scal[6] = feb_hi; }
+      fcount = block_all(fcount, [](int x, int y) { return x + y; }, sh.ired, 0);
+      eb_lo = b.scal[5];
+      eb_hi = b.scal[6];
+      __syncthreads();
+      if (fcount == 0 || fcount > GATHER_CAP) return false;
+      f_lo += int(base);  // absolute fine indices from here on
+      f_hi += int(base);
+    }
+    // The gathering pass (the second one for a dense range): the tokens of
+    // the boundary's bins, and the pick over the ones before them not picked yet.
+    const double fine_from = dense ? double(f_lo) : 0.0;
+    auto gather_group = [&](int g, const W (&x)[4], uint32_t bits) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const W v = x[j];
+        if (!(((bits >> j) & 1u) && v > neg_inf<W>())) continue;
+        const float x32 = tp.x32(v);
+        if (x32 < edge_range - SCREEN || x32 > edge_before + SCREEN) continue;
+        const double k = coarse_of(v);
+        if (k < double(b_lo) || k > double(b_hi) || !tp.kept(v, x32)) continue;
+        if (dense) {
+          const double f = fine_top - floor(double(v) * inv4 * FINE_PER_COARSE);
+          if (f < fine_from || f > double(f_hi)) continue;
+        }
+        const int slot = atomicAdd(&b.n, 1);
+        if (slot < GATHER_CAP) keys[slot] = gkey(v, 4 * g + j);
+      }
+    };
+    if (dense) {
+      // Only the coarse range's tokens before f_lo still need the pick.
+      auto keep_fine = [&](W v, float x) {
+        if (x < edge_range - SCREEN || x > edge_before + SCREEN || !tp.kept(v, x)) return false;
+        const double k = coarse_of(v);
+        if (k < double(b_lo) || k > double(b_hi)) return false;
+        return fine_top - floor(double(v) * inv4 * FINE_PER_COARSE) < fine_from;
+      };
+      each_group([&](int g, const W (&x)[4], uint32_t bits) {
+        gather_group(g, x, bits);
+        pick_group<false>(g, x, bits, tp, p.rng, sub, excluded, keep_fine, best, bar, nullptr);
+      }, share_bar);
+    } else {
+      each_group([&](int g, const W (&x)[4], uint32_t bits) {
+        gather_group(g, x, bits);
+        if (b_lo > 0) pick_group<false>(g, x, bits, tp, p.rng, sub, excluded, keep_before, best, bar, nullptr);
+      }, share_bar);
+    }
+    __syncthreads();
+    const int n = b.n;
+    if (n == 0 || n > GATHER_CAP) return false;
+    // ---- 3. The boundary among the gathered tokens. ----
+    int n_pad = 64;
+    while (n_pad < n) n_pad <<= 1;
+    for (int i = n + tid; i < n_pad; i += BLOCK) keys[i] = GKey(0);
+    block_sort_desc(keys, n_pad);
+    for (int i = tid; i < n; i += BLOCK) wts[i] = exp(tp.x64(gvalue(keys[i])));
+    __syncthreads();
+    // Thread t owns sorted entries [per t, per t + per): inclusive
+    // double-double prefix sums of the FP64 weights, in order. A pass finds
+    // the first entry whose prefix (plus the mass before, in [elo, ehi])
+    // certainly reaches the target interval [tlo, thi] and the first that
+    // may, and records entry `want`'s prefix bounds in sh.sp_lo / sh.sp_hi;
+    // the whole sum and its bound go to sh.sp_mid / sh.sp_others.
+    const int per = (n_pad + BLOCK - 1) / BLOCK;
+    auto mn = [](int x, int y) { return x < y ? x : y; };
+    auto prefix_pass = [&](double tlo, double thi, double elo, double ehi, int want, int* first_yes,
+                           int* first_unsure) {
+      DD local{0, 0};
+      for (int u = 0; u < per; ++u) {
+        const int i = per * tid + u;
+        if (i < n) local = dd_add(local, DD{wts[i], 0});
+      }
+      const DD inc = wave_scan(local, [](DD x, DD y) { return dd_add(x, y); }, DD{0, 0});
+      __syncthreads();
+      if (lane == WAVE - 1) sh.ddred[wid] = inc;
+      __syncthreads();
+      DD run{0, 0};
+      for (int w = 0; w < wid; ++w) run = dd_add(run, sh.ddred[w]);
+      run = dd_add(run, dd_add(inc, DD{-local.hi, -local.lo}));
+      int fy = INT_MAX, fu = INT_MAX;
+      for (int u = 0; u < per; ++u) {
+        const int i = per * tid + u;
+        if (i >= n) break;
+        run = dd_add(run, DD{wts[i], 0});
+        const double err = dd_sum_error(run, i + 1) + 4 * 0x1p-104 * run.hi;
+        const int yes = dd_reaches(dd_add(run, DD{elo, 0}), err, thi);
+        const int no = dd_reaches(dd_add(run, DD{ehi, 0}), err, tlo);
+        if (yes == 1) fy = min(fy, i);
+        else if (no != 0) fu = min(fu, i);
+        if (i == want) {
+          sh.sp_lo = (run.hi + elo + run.lo - err) * (1 - 0x1p-50);
+          sh.sp_hi = (run.hi + ehi + run.lo + err) * (1 + 0x1p-50);
+        }
+        if (i == n - 1) {
+          sh.sp_mid = run.hi + run.lo;
+          sh.sp_others = err + 0x1p-100 * run.hi;
+        }
+      }
+      *first_yes = block_all(fy, mn, sh.ired, INT_MAX);
+      *first_unsure = block_all(fu, mn, sh.ired, INT_MAX);
+    };
+    int first_yes, first_unsure;
+    prefix_pass(lo_t, hi_t, eb_lo, eb_hi, -1, &first_yes, &first_unsure);
+    // The total refined: the gathered weights' sum (near exact) and the
+    // bounded mass outside the coarse range. When the total's rounding is then
+    // certain (both bounds strictly inside one double's rounding interval,
+    // tested with exact differences) the target is exact: the oracle's
+    // top_p * fsum(kept).
+    if (!dense) {
+      const double lo = (sh.sp_mid - sh.sp_others + rest_lo) * (1 - 0x1p-51);
+      const double hi = (sh.sp_mid + sh.sp_others + rest_hi) * (1 + 0x1p-51);
+      __syncthreads();
+      if (lo > 0 && lo <= hi) {
+        const double d = 0.5 * lo + 0.5 * hi;
+        const double down = d - nextafter(d, 0.0), up = nextafter(d, INFINITY) - d;
+        if (lo - d > -0.5 * down && hi - d < 0.5 * up) {
+          lo_t = hi_t = p.top_p * d;
+        } else {
+          lo_t = fmax(lo_t, p.top_p * lo * (1 - 0x1p-50));
+          hi_t = fmin(hi_t, p.top_p * hi * (1 + 0x1p-50));
+        }
+      }
+    }
+    prefix_pass(lo_t, hi_t, eb_lo, eb_hi, -1, &first_yes, &first_unsure);
+    // The correctly rounded sum of the first m gathered weights (LDS superaccumulator).
+    auto rounded_prefix = [&](int m) {
+      sacc_clear(sh.limbs);
+      __syncthreads();
+      for (int i = tid; i < m; i += BLOCK) sacc_add(sh.limbs, wts[i]);
+      __syncthreads();
+      if (wid == 0) {
+        const double r = sacc_round_wave(sh.limbs);
+        if (lane == 0) sh.dred[0] = r;
+      }
+      __syncthreads();
+      const double r = sh.dred[0];
+      __syncthreads();
+      return r;
+    };
+    int cut_i;
+    bool den_exact = false;
+    double den = 0;
+    if (first_unsure < first_yes) {
+      // Settled exactly only when nothing precedes the gathered tokens: the
+      // correctly rounded total gives the target, and exact prefix sums of
+      // the gathered weights decide the uncertain entries in order.
+      if (b_lo != 0 || dense) return false;
+      double target;
+      if (lo_t == hi_t) {
+        target = lo_t;
+      } else {
+        ++fallbacks;
+        const double total = exact_sum<false>([&](int, W v, bool ok) -> double {
+          return valid_tok(v, ok) && tp.kept(v, tp.x32(v)) ? exp(tp.x64(v)) : 0.0;
+        }, false);
+        target = p.top_p * total;
+        prefix_pass(target, target, 0.0, 0.0, -1, &first_yes, &first_unsure);
+      }
+      cut_i = first_yes;
+      for (int i = first_unsure; i < first_yes; ++i) {
+        const double r = rounded_prefix(i + 1);
+        if (r >= target) { cut_i = i; den = r; den_exact = true; break; }
+      }
+      if (cut_i == INT_MAX) return false;
+      if (!den_exact) { den = rounded_prefix(cut_i + 1); den_exact = true; }
+    } else {
+      if (first_yes == INT_MAX) return false;
+      cut_i = first_yes;
+    }
+    // The nucleus mass: the prefix through the cut, with its bounds.
+    if (!den_exact) prefix_pass(lo_t, hi_t, eb_lo, eb_hi, cut_i, &first_yes, &first_unsure);
+    __syncthreads();
+    out->cut = u128(keys[cut_i]);
+    out->den_exact = den_exact;
+    out->den_lo = den_exact ? den : sh.sp_lo;
+    out->den_hi = den_exact ? den : sh.sp_hi;
+    // The pick over the gathered part of the nucleus, joined with the pick before it.
+    for (int i = tid; i <= cut_i; i += BLOCK) {
+      const W v = gvalue(keys[i]);
+      const int t = gid(keys[i]);
+      if (t == excluded) continue;
+      const float x = tp.x32(v), g = gumbel32(word_of(p.rng, sub, uint32_t(t))), sc = x + g;
+      const float e = SCORE_ERR * (1.f + fabsf(x) + fabsf(g));
+      best = pick_join(best, Pick{sc, sc - e, sc + e, -INFINITY, t});
+    }
+    out->pick = block_pick(best, sh);
+    return true;
+  }
+
   // Certified FP32 draw over tokens where in(t, v, ok) holds (excluded
   // removed), FP64 rescoring when the certificate fails. floor_id is a token
   // certainly in the set (or -1).
@@ -1607,18 +2283,39 @@ template <int DT, bool VEC> struct FullRow {
     // ---- Top-k: an exact cut at the k-th token (reference.py:67-71). ----
     // The kept count is needed only when k may cut: k < valid tokens.
     u128 cut = 0;  // keep ck >= cut
+    bool topk_cut = false;
     if (p.top_k > 0 && p.top_k < valid) {
       int nk = 0;
       each<false>([&](int t, W v, bool ok) { nk += kept(t, v, ok); });
       nk = block_all(nk, [](int x, int y) { return x + y; }, sh.ired, 0);
-      if (p.top_k < nk) cut = select_nth(int(p.top_k), kept);
+      if (p.top_k < nk) {
+        cut = select_nth(int(p.top_k), kept);
+        topk_cut = true;
+      }
     }
     auto in_k = [&](int t, W v, bool ok) { return kept(t, v, ok) && CK<W>::make(v, t) >= cut; };
     auto w64 = [&](int, W v) -> double { return exp(tp.x64(v)); };
     double den = 0;
     bool den_exact = false;
+    // The floor of a draw: the first token of the order that the draw may take.
+    const int floor_token = greedy >= 0 && greedy < int(a.vocab) ? greedy : -1;
+    // The residual's floor: the greedy token, or the runner-up when the draft is greedy.
+    const int residual_floor = p.draft_id == greedy ? (runner_up_id != INT_MAX ? runner_up_id : -1) : floor_token;
     // ---- Top-p: the shortest prefix whose fsum reaches top_p * fsum(all) (reference.py:73-85). ----
-    if (p.top_p < 1) {
+    bool binned = false;  // the cut, its mass bounds and the draw's pick come from the bins
+    BinnedCut bc;
+    if (p.top_p < 1 && !topk_cut && !full_q && tb) {
+      binned = topp_binned(p.verify ? 2u : 0u, p.verify ? p.draft_id : -1, p.verify ? residual_floor : floor_token,
+                           &bc);
+      if (binned) {
+        cut = bc.cut;
+        den = bc.den_lo;
+        den_exact = bc.den_exact;
+      }
+    }
+    // A pick that settles the draw: certified, or certainly empty.
+    auto settled = [](const Pick& pk) { return pk.id == INT_MAX ? !(pk.others > -INFINITY) : pk.lo > pk.others; };
+    if (p.top_p < 1 && !binned) {
       cut = mass_boundary(p.top_p, in_k, w64);
       // The kept mass is needed by the ratio test and the residual only: a
       // draw compares x + G, the same for every token up to log(den).
@@ -1630,8 +2327,6 @@ template <int DT, bool VEC> struct FullRow {
       }
     }
     auto in_final = [&](int t, W v, bool ok) { return in_k(t, v, ok) && CK<W>::make(v, t) >= cut; };
-    // The floor of a draw: the first token of the order that the draw may take.
-    const int floor_token = greedy >= 0 && greedy < int(a.vocab) ? greedy : -1;
     // ---- Ratio test (reference.py:229-230). ----
     if (p.verify) {
       const W vx = view.value(p.draft_id);
@@ -1639,7 +2334,20 @@ template <int DT, bool VEC> struct FullRow {
       const double u = uniform64(word_of(p.rng, 1u, 0u));
       bool accept = false;
       if (x_in) {
-        if (!den_exact) {
+        if (binned && !den_exact) {
+          // The nucleus mass bounds from the bins first.
+          const double wx = exp(tp.x64(vx));
+          const double rlo = fmin(1.0, wx / bc.den_hi) * (1 - 1e-12), rhi = fmin(1.0, wx / bc.den_lo) * (1 + 1e-12);
+          const bool bounded = bc.den_lo > 0 && bc.den_hi >= bc.den_lo;
+          if (bounded && u < rlo) accept = true;
+          else if (bounded && u >= rhi) accept = false;
+          else {
+            den = exact_sum<false>([&](int t, W v, bool ok) -> double { return in_final(t, v, ok) ? w64(t, v) : 0.0; }, false);
+            den_exact = true;
+            ++fallbacks;
+            accept = u < fmin(1.0, wx / den);
+          }
+        } else if (!den_exact) {
           // FP32 sum of kept weights with its bound first.
           float s = 0, c = 0, e = 0;
           int pruned = 0;
@@ -1676,7 +2384,11 @@ template <int DT, bool VEC> struct FullRow {
       r.p = accept ? 1.0 : 0.0;
       if (accept) return r;
       if (!full_q) {
-        const int floor_id = p.draft_id == greedy ? (runner_up_id != INT_MAX ? runner_up_id : -1) : greedy;
+        if (binned && settled(bc.pick)) {
+          r.residual = bc.pick.id == INT_MAX ? -1 : bc.pick.id;
+          return r;
+        }
+        const int floor_id = residual_floor;
         int fl = floor_id >= 0 && floor_id < int(a.vocab) ? floor_id : -1;
         if (fl >= 0 && fl != greedy) {
           const W vf = view.value(fl);
@@ -1713,124 +2425,14 @@ template <int DT, bool VEC> struct FullRow {
       r.residual = res.id == INT_MAX ? -1 : res.id;
       return r;
     }
+    if (binned && settled(bc.pick)) {
+      r.sample = bc.pick.id == INT_MAX ? -1 : bc.pick.id;
+      return r;
+    }
     r.sample = draw(0, -1, floor_token, in_final);
     return r;
   }
 };
-
-// ---------------------------------------------------------------------------
-// The streaming draw of stream rows (reference: fused.cuh:532-681 row_scan and
-// its Pick merge :301-314).
-template <class SH> __device__ __forceinline__ Pick block_pick(Pick pk, SH& sh) {
-  pk = wave_all(pk, pick_join, pick_none());
-  __syncthreads();
-  if (lane_id() == 0) sh.picks[wave_id()] = pk;
-  __syncthreads();
-  Pick r = sh.picks[0];
-#pragma unroll
-  for (int w = 1; w < WAVES; ++w) r = pick_join(r, sh.picks[w]);
-  __syncthreads();
-  return r;
-}
-
-// A thread's Kahan sum of exp(x) over kept tokens with x >= SUM_PRUNE, its
-// error bound term, and the count of kept tokens below SUM_PRUNE.
-struct KahanSum {
-  float s = 0.f, c = 0.f, e = 0.f;
-  int pruned = 0;
-  __device__ __forceinline__ void add(float x) {
-    if (!(x >= SUM_PRUNE)) { ++pruned; return; }
-    const float w = weight32(x), d = w - c, t = s + d;
-    c = (t - s) - d;
-    s = t;
-    e += w * (X_ERR * (1.f + fabsf(x)));
-  }
-};
-
-// One group of four tokens into a thread's certified pick: tokens whose bit
-// is set in `bits`, above -inf, not `excluded` and passing keep(v, x), scored
-// x + G(word(sub, t)) with x = tp.x32(v). A token whose score bound stays
-// under `bar` (the floor, then the thread's best lower bound) needs no Philox
-// word; one Philox call serves the group's four tokens. With SUM, every such
-// token (the excluded one too) also goes into `sum`.
-template <bool SUM, class W, class Keep>
-__device__ __forceinline__ void pick_group(int g, const W (&x)[4], uint32_t bits, const Temp<W>& tp,
-                                           const RngAddr& rng, uint32_t sub, int excluded, Keep&& keep, Pick& best,
-                                           float& bar, KahanSum* sum) {
-  float xs[4];
-  uint32_t live = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const W v = x[j];
-    xs[j] = tp.x32(v);
-    const bool ok = ((bits >> j) & 1u) && v > neg_inf<W>() && keep(v, xs[j]);
-    if constexpr (SUM) {
-      if (ok) sum->add(xs[j]);
-    }
-    if (!ok || 4 * g + j == excluded) continue;
-    const float ub = xs[j] + GUMBEL_MAX + SCORE_ERR * (1.f + fabsf(xs[j]) + GUMBEL_MAX);
-    if (ub < bar) {
-      best.others = fmaxf(best.others, ub);
-      continue;
-    }
-    live |= 1u << j;
-  }
-  if (!live) return;
-  const Words w4 = philox(rng.seed, rng.stream, rng.position, sub, uint32_t(g));
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if (!((live >> j) & 1u)) continue;
-    const uint32_t w = w4.w[j];
-    const float gb = gumbel_upper(w);
-    const float ub2 = xs[j] + gb + SCORE_ERR * (1.f + fabsf(xs[j]) + fabsf(gb));
-    if (ub2 < bar) {
-      best.others = fmaxf(best.others, ub2);
-      continue;
-    }
-    const float G = gumbel32(w), sc = xs[j] + G, e = SCORE_ERR * (1.f + fabsf(xs[j]) + fabsf(G));
-    const int t = 4 * g + j;
-    if (sc > best.mid || (sc == best.mid && t < best.id)) {
-      best.others = fmaxf(best.others, best.hi);
-      best = Pick{sc, sc - e, sc + e, best.others, t};
-    } else {
-      best.others = fmaxf(best.others, sc + e);
-    }
-    bar = fmaxf(bar, best.lo - PRUNE_MARGIN);
-  }
-}
-
-// The thread's certified pick over the allowed tokens of groups [g_begin,
-// g_end) read from memory, B groups in flight per thread (thread k takes
-// g_begin + k, + BLOCK, ...).
-template <int B, bool SUM, int DT, bool VEC, class Keep>
-__device__ __forceinline__ Pick range_pick(const es_arguments& a, int64_t row, const RowView<DT, VEC>& view,
-                                           int g_begin, int g_end, const Temp<typename Ty<DT>::W>& tp,
-                                           const RngAddr& rng, uint32_t sub, int excluded, float floor, Keep&& keep,
-                                           KahanSum* sum) {
-  using W = typename Ty<DT>::W;
-  Pick best = pick_none();
-  float bar = floor - PRUNE_MARGIN;
-  // Every lane runs the same number of rounds (groups past the range carry no
-  // tokens), so after each round the wave can share its best lower bound: a
-  // token whose upper bound stays below it cannot win, and is kept only as a
-  // loser's bound, as with the thread's own best.
-  for (int base0 = g_begin; base0 < g_end; base0 += B * BLOCK) {
-    const int base = base0 + int(threadIdx.x);
-    W x[B][4];
-    uint32_t mb[B];
-#pragma unroll
-    for (int u = 0; u < B; ++u) {
-      const int g = base + u * BLOCK;
-      view.load(min(g, g_end - 1), x[u]);
-      mb[u] = g < g_end ? group_bits(a, row, g) : 0u;
-    }
-#pragma unroll
-    for (int u = 0; u < B; ++u) pick_group<SUM>(base + u * BLOCK, x[u], mb[u], tp, rng, sub, excluded, keep, best, bar, sum);
-    const float wave_lo = wave_all(best.lo, [](float p, float q) { return p > q ? p : q; }, -INFINITY);
-    bar = fmaxf(bar, wave_lo - PRUNE_MARGIN);
-  }
-  return best;
-}
 
 // A stream row's slice: its certified draw over the slice's tokens that may
 // be kept, read again from memory (cache hits), stored where a list row keeps
@@ -2196,6 +2798,87 @@ __device__ __forceinline__ void write_part(const es_arguments& a, int64_t row, i
   slice_parts(a, row)[slice] = part;
 }
 
+// A binned top-p row's slice (reference: fused.cuh:686-750, row_hist, whose
+// distance histogram and kept-mass sum this replaces): every valid token of
+// the slice is binned on the absolute grid y = l * 4 / T against a reference
+// maximum m_ref (the slice's, or the largest slice maximum of the row
+// published so far, a lower bound on the row maximum): bin b = floor(y) at
+// local index floor(m_ref * 4 / T) - b. The 64 bins below m_ref get the count
+// and the sum of e^((y - b - 1/2) / 4) in FP64 (the weights relative to the
+// bin's centre, a degree-11 polynomial); tokens further down go to an FP32
+// Kahan sum of their weights relative to m_ref with the certified bound
+// (tokens below e^-40 are bounded by the largest of them). Returns false (the
+// row then takes the full-row path's radix boundary) when m_ref * 4 / T is
+// out of range for the grid.
+struct SliceBins { double mref, top, far_sum, far_err; };
+template <int DT, bool VEC, class W>
+__device__ __forceinline__ bool slice_bins(const es_arguments& a, int64_t row, int slice, const Params& p,
+                                           const RowView<DT, VEC>& view, int g0, int g1, W smax, uint32_t gen,
+                                           Shared<W>& sh, SliceBins* out) {
+  const int tid = threadIdx.x;
+  unsigned long long* key = &counters(a, row)->max_key;
+  double* lmass = reinterpret_cast<double*>(&sh.u);
+  unsigned* lcnt = reinterpret_cast<unsigned*>(lmass + TP_COARSE);
+  if (tid == 0) {
+    publish_max(key, gen, order_key(float_at_or_below(double(smax))));
+    sh.dred[0] = published_max(key, gen);
+  }
+  if (tid < TP_COARSE) {
+    lmass[tid] = 0;
+    lcnt[tid] = 0;
+  }
+  __syncthreads();
+  const double mref = fmax(double(smax), sh.dred[0]);
+  const double inv4 = TP_Y_PER_X / p.temperature;
+  const double yref = mref * inv4;
+  if (!(fabs(yref) < 0x1p50)) return false;
+  const double top = floor(yref);
+  Temp<W> ts;
+  ts.init(mref, p.temperature, 0.0);
+  KahanSum ks;
+  for (int base = g0 + tid; base < g1; base += 4 * BLOCK) {
+    W x[4][4];
+    uint32_t mb[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int g = base + u * BLOCK;
+      view.load(min(g, g1 - 1), x[u]);
+      mb[u] = g < g1 ? group_bits(a, row, g) : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const W v = x[u][j];
+        if (!(((mb[u] >> j) & 1u) && v > neg_inf<W>())) continue;
+        const double y = double(v) * inv4, b = floor(y), k = top - b;
+        if (k < double(TP_COARSE)) {
+          atomicAdd(&lmass[int(k)], exp_center((y - b - 0.5) * (1.0 / TP_Y_PER_X)));
+          atomicAdd(&lcnt[int(k)], 1u);
+        } else {
+          ks.add(ts.x32(v));
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < TP_COARSE) {
+    slice_bin_mass(a, row, slice)[tid] = lmass[tid];
+    slice_bin_count(a, row, slice)[tid] = uint16_t(lcnt[tid]);
+  }
+  const double sum = block_all(double(ks.s) - double(ks.c), [](double x, double y) { return x + y; }, sh.dred, 0.0);
+  const double e = block_all(double(ks.e), [](double x, double y) { return x + y; }, sh.dred, 0.0);
+  const int pruned = block_all(ks.pruned, [](int x, int y) { return x + y; }, sh.ired, 0);
+  const float pmax = block_all(ks.pruned_max, [](float x, float y) { return x > y ? x : y; }, sh.fred, -INFINITY);
+  out->mref = mref;
+  out->top = top;
+  out->far_sum = sum;
+  // The FP32 terms' bound, the Kahan sums' and the block's FP64 tree; the
+  // tokens left out are each below e^(x32 (1 - 1e-6)).
+  out->far_err = 1.01 * e + 4.8e-7 * sum + (pruned ? double(pruned) * exp(double(pmax) * (1 - 1e-6)) : 0.0);
+  return true;
+}
+
 // es_wide, the slice pass of a call whose rows need more than MAX_SLICES
 // register tiles (launched in place of es_main): each slice of several tiles
 // is read group by group for the statistics (NaN/+inf anywhere, the valid
@@ -2339,7 +3022,7 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(5)))
   Params p;
   slice_params(a, row, slice, x0, x1, &p, sh);
   if (p.status != ES_OK) return;
-  const ListPlan lp = list_plan(p, a.list_max, pl.cap_slice, a.vocab);
+  const ListPlan lp = list_plan(p, a.list_max, pl.cap_slice, a.vocab, pl.slices);
   int need = lp.need;
   const int L = lp.L;
   const bool sorted_list = lp.sorted_list, need_topp = lp.need_topp;
@@ -2576,14 +3259,13 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(5)))
       fid = -1;
     }
     // Top-p lists also need the kept weights' sum, relative to the slice
-    // maximum, in FP64: each weight exp((l - max) / T) within 5e-15 of its
-    // value (|x| <= 40 for the terms summed), Kahan sums per thread and a
-    // block tree; 1e-14 S bounds the error. Weights below e^-40 are counted,
-    // not summed.
+    // maximum: FP32 weights and Kahan sums per thread with the certified
+    // bound (as the streaming draw's ratio rows), an FP64 block tree. Weights
+    // below e^-40 are counted, not summed.
     if (need_topp) {
-      const double ms = double(smax), T = p.temperature;
-      double s = 0, c = 0;
-      int pr = 0;
+      Temp<W> ts;
+      ts.init(double(smax), p.temperature, 0.0);
+      KahanSum ks;
       for (int base = g0 + tid; base < g1; base += 4 * BLOCK) {
         W x[4][4];
         uint32_t mb[4];
@@ -2597,21 +3279,27 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(5)))
         for (int u = 0; u < 4; ++u) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const bool ok = ((mb[u] >> j) & 1u) && x[u][j] > neg_inf<W>();
-            const double xl = (double(x[u][j]) - ms) / T;
-            const bool counted = ok && xl >= double(SUM_PRUNE);
-            pr += ok && !counted;
-            if (counted) {
-              const double d = exp(xl) - c, t2 = s + d;
-              c = (t2 - s) - d;
-              s = t2;
-            }
+            if (((mb[u] >> j) & 1u) && x[u][j] > neg_inf<W>()) ks.add(ts.x32(x[u][j]));
           }
         }
       }
-      psum = block_all(s - c, [](double x, double y) { return x + y; }, sh.dred, 0.0);
-      perr = 1e-14 * psum;
-      pruned = block_all(pr, [](int x, int y) { return x + y; }, sh.ired, 0);
+      psum = block_all(double(ks.s) - double(ks.c), [](double x, double y) { return x + y; }, sh.dred, 0.0);
+      // The FP32 terms' bound, the Kahan sums' and the block's FP64 tree.
+      perr = 1.01 * block_all(double(ks.e), [](double x, double y) { return x + y; }, sh.dred, 0.0) + 4.8e-7 * psum;
+      pruned = block_all(ks.pruned, [](int x, int y) { return x + y; }, sh.ired, 0);
+    }
+  } else if (lp.binned && !bad && valid > 0) {
+    // A binned top-p row: the slice's bins (n_cand TP_COARSE marks them
+    // usable), its top bin in `frontier`, its reference maximum in `tau`.
+    SliceBins sb;
+    if (slice_bins<DT, VEC>(a, row, slice, p, view, g0, g1, smax, pl.generation, sh, &sb)) {
+      tau = sb.mref;
+      frontier = sb.top;
+      psum = sb.far_sum;
+      perr = sb.far_err;
+      n_cand = TP_COARSE;
+    } else {
+      n_cand = -1;
     }
   } else if (a.dispatch != 1 && stream_row(p, a.vocab) && !bad && valid > 0) {
     const SliceDraw sd = slice_draw<DT, VEC>(a, row, slice, p, view, g0, g1, double(smax), first_id, pl.cap_slice,
@@ -2708,6 +3396,7 @@ template <int DT, bool VEC>
 __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments, Plan) {
   using W = typename Ty<DT>::W;
   __shared__ Shared<W> sh;
+  __shared__ TopPBins tbins;  // the full-row path's binned top-p boundary
   const es_arguments& a = kernel_args().a;
   const Plan pl = kernel_args().pl;
   if (int64_t(blockIdx.x) >= a.rows) {
@@ -2745,7 +3434,7 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments, Plan) {
     return;
   }
   const int list_max = a.list_max;
-  const ListPlan lp = list_plan(p, list_max, pl.cap_slice, a.vocab);
+  const ListPlan lp = list_plan(p, list_max, pl.cap_slice, a.vocab, pl.slices);
   const bool sorted_list = lp.sorted_list, need_topp = lp.need_topp;
   const bool stream = a.dispatch != 1 && stream_row(p, a.vocab);  // dispatch 1: the full-row path
   const bool stream_sum = stream && stream_sub(p) == 2u;  // the ratio test needs the kept mass
@@ -2869,6 +3558,8 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments, Plan) {
       done = stream_finish<DT, VEC>(a, row, p, pl, sh, &result, &why);
     } else if (sorted_list && sh.wdone < 0) {
       why = 7;  // a rounding the wave could not certify: the full-row path decides
+    } else if (lp.binned) {
+      why = 10;  // a binned top-p row: the full-row path from the slices' bins
     } else if (p.temperature > 0 && !p.full_q && list_max > 0) {
       const int valid_all = sh.valid;
       const int n_keep = p.top_k > 0 && p.top_k < valid_all ? int(p.top_k) : valid_all;
@@ -2885,7 +3576,12 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments, Plan) {
       const double maximum = sh.maximum;
       const int greedy = sh.greedy, runner_up_id = sh.runner_up_id, valid = sh.valid;
       __syncthreads();
-      FullRow<DT, VEC> full(a, row, p, sh, pl.groups);
+      FullRow<DT, VEC> full(a, row, p, sh, pl.groups, &tbins);
+      if (lp.binned) {
+        int usable = 1;
+        for (int sl = 0; sl < pl.slices; ++sl) usable &= sh.n_cand[sl] == TP_COARSE;
+        full.bin_slices = usable ? pl.slices : 0;
+      }
       result = full.run(maximum, greedy, runner_up_id, valid);
       result.target_status = ES_OK;
       fallbacks += full.fallbacks;

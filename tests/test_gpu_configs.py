@@ -289,3 +289,15 @@ def test_full_ragged_configuration(config5_full, variant):
 def test_flatness_rows_one_at_a_time(filt, row):
     """Rows 0, 10 and 90 are the constructed ones (a threshold within an ulp)."""
     _run(bench.config3_single(filt=filt, row=row))
+
+
+# ---- Top-p with large nuclei: the reference benchmark's T = 0.7, top-p 0.9 setting. ----
+@pytest.mark.parametrize("list_max", [256, 0])
+@pytest.mark.parametrize("cell", ["128x1_T0.7_p0.9", "64x5_T0.7_p0.9"])
+def test_top_p_cells_match_the_oracle(cell, list_max):
+    """Nuclei of 1 to about 9,000 tokens (median 225): small ones finish as
+    lists, large ones on the full-row path's binned boundary; list_max 0
+    sends every row to the full-row path."""
+    args = _run(bench.CELLS[cell](), list_max=list_max)
+    routes = _routes(args)
+    assert all(r in (3, 4) or r >= 100 for r in routes), sorted(set(routes))
