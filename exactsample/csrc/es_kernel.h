@@ -1365,11 +1365,106 @@ __device__ __forceinline__ double exp_near_zero(double d) {
 
 // The row's bins (es_finish only; the gathered tokens of the boundary bins
 // live in the block's list union).
+// A wave's queue of groups whose tokens may win a Gumbel-max draw, drained
+// 64 at a time with one group per lane (see DensePick).
+constexpr int PQ_CAP = 128;
+struct PickQueue {
+  int g[WAVES][PQ_CAP];          // group
+  uint32_t live[WAVES][PQ_CAP];  // its candidates (bit j: token 4 g + j)
+};
+
 struct TopPBins {
   double mass[TP_BINS];   // sum over the bin's kept tokens of their weights relative to the bin's centre
   unsigned cnt[TP_BINS];  // kept tokens in the bin
   double scal[TP_SCALARS];
   int n;                  // tokens gathered
+  PickQueue pq;
+};
+
+// A certified FP32 Gumbel-max over groups of four tokens whose Philox block
+// is computed densely: lanes queue the groups that hold candidates (a group
+// index and a 4-bit mask), and once 64 groups are queued the wave draws them
+// one group per lane: it reads the group's four values again (cache hits),
+// computes one Philox call for them, screens each candidate with the cheap
+// bound and, if that reaches the bar, computes the accurate noise; then it
+// shares its best lower bound as the new bar. Scattered candidates thus cost
+// a Philox call per group instead of one per wave step, and the streaming
+// loop that finds them stays free of the draw's code. Every lane calls every
+// member.
+struct DensePick {
+  Pick best;
+  float bar;
+  int n;  // queued (wave-uniform)
+  __device__ __forceinline__ void init(float floor) {
+    best = pick_none();
+    bar = floor - PRUNE_MARGIN;
+    n = 0;
+  }
+  // Queues group g if `cand` (bit j: token 4 g + j) is not empty.
+  __device__ __forceinline__ void offer(PickQueue& q, int g, uint32_t cand) {
+    const uint64_t has = __ballot(cand != 0);
+    if (!has) return;
+    const int w = wave_id();
+    const int pos = n + __popcll(has & ((1ull << lane_id()) - 1ull));
+    if (cand) {
+      q.g[w][pos] = g;
+      q.live[w][pos] = cand;
+    }
+    n += __popcll(has);
+  }
+  // Draws queued groups once 64 are waiting (or all of them with `all`);
+  // xs_of(g, xs) gives the FP32 x of group g's four tokens.
+  template <class XsOf>
+  __device__ __forceinline__ void drain(PickQueue& q, const RngAddr& rng, uint32_t sub, bool all, XsOf&& xs_of) {
+    const int w = wave_id(), lane = lane_id();
+    while (n >= WAVE || (all && n > 0)) {
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      const int take = min(n, WAVE);
+      if (lane < take) {
+        const int g = q.g[w][lane];
+        const uint32_t live = q.live[w][lane];
+        float xs[4];
+        xs_of(g, xs);
+        const Words w4 = philox(rng.seed, rng.stream, rng.position, sub, uint32_t(g));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (!((live >> j) & 1u)) continue;
+          const uint32_t word = w4.w[j];
+          const float gb = gumbel_upper(word);
+          const float ub2 = xs[j] + gb + SCORE_ERR * (1.f + fabsf(xs[j]) + fabsf(gb));
+          if (ub2 < bar) {
+            best.others = fmaxf(best.others, ub2);
+            continue;
+          }
+          const float G = gumbel32(word), sc = xs[j] + G, e = SCORE_ERR * (1.f + fabsf(xs[j]) + fabsf(G));
+          const int t = 4 * g + j;
+          if (sc > best.mid || (sc == best.mid && t < best.id)) {
+            best.others = fmaxf(best.others, best.hi);
+            best = Pick{sc, sc - e, sc + e, best.others, t};
+          } else {
+            best.others = fmaxf(best.others, sc + e);
+          }
+          bar = fmaxf(bar, best.lo - PRUNE_MARGIN);
+        }
+      }
+      // Move the rest to the front (at most 63 entries) and share the bar.
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      const int rest = n - take;
+      int g2 = 0;
+      uint32_t l2 = 0;
+      if (lane < rest) {
+        g2 = q.g[w][take + lane];
+        l2 = q.live[w][take + lane];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      if (lane < rest) {
+        q.g[w][lane] = g2;
+        q.live[w][lane] = l2;
+      }
+      n = rest;
+      bar = fmaxf(bar, wave_all(best.lo, [](float u, float v) { return u > v ? u : v; }, -INFINITY) - PRUNE_MARGIN);
+    }
+  }
 };
 
 // Sorts keys[0, n) descending in the block (bitonic, n a power of two >= 64;
@@ -1722,7 +1817,9 @@ template <int DT, bool VEC> struct FullRow {
   // group processed at a time (the loaded groups rotate through a fixed
   // register slot, keeping the loop body to one copy): f(g, x, bits) per
   // group, then round() once per round, in every lane.
+  static constexpr int TGP = 16;  // groups of four in flight per thread in each_group
   template <class F, class R> __device__ __forceinline__ void each_group(F&& f, R&& round) const {
+    constexpr int TG = TGP;
     for (int base0 = 0; base0 < groups; base0 += BLOCK * TG) {
       const int base = base0 + int(threadIdx.x);
       W x[TG][4];
@@ -1866,10 +1963,36 @@ template <int DT, bool VEC> struct FullRow {
         floor_score = x + g - SCORE_ERR * (1.f + fabs(x) + fabsf(g));
       }
     }
-    Pick best = pick_none();
-    float bar = floor_score - PRUNE_MARGIN;
-    auto share_bar = [&]() {
-      bar = fmaxf(bar, wave_all(best.lo, [](float u, float v) { return u > v ? u : v; }, -INFINITY) - PRUNE_MARGIN);
+    DensePick dp;
+    dp.init(floor_score);
+    auto xs_of = [&](int g, float (&xs)[4]) {
+      W v[4];
+      view.load(g, v);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xs[j] = tp.x32(v[j]);
+    };
+    // The streaming loop records each group's candidates (tokens where
+    // keep(v, x) holds, the draft left out) in round_cand, 4 bits per group
+    // of the round; after the round the groups are queued for the draw.
+    uint64_t round_cand = 0;
+    int round_base = tid;  // the first group of the current round for this thread
+    auto candidates = [&](int g, const W (&x)[4], uint32_t bits, auto&& keep) {
+      uint32_t cand = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const W v = x[j];
+        if (((bits >> j) & 1u) && v > neg_inf<W>() && 4 * g + j != excluded && keep(v, tp.x32(v))) cand |= 1u << j;
+      }
+      const int u = (g - round_base) / BLOCK;  // the group's place in the round
+      round_cand |= uint64_t(cand) << (4 * u);
+    };
+    auto end_round = [&]() {
+      for (int u = 0; u < TGP; ++u) {
+        dp.offer(b.pq, round_base + u * BLOCK, uint32_t(round_cand >> (4 * u)) & 0xfu);
+        dp.drain(b.pq, p.rng, sub, false, xs_of);
+      }
+      round_cand = 0;
+      round_base += BLOCK * TGP;
     };
     auto keep_before = [&](W v, float x) { return tp.kept(v, x) && before_range(v, x); };
     const bool dense = count > GATHER_CAP;
@@ -1897,8 +2020,8 @@ template <int DT, bool VEC> struct FullRow {
           atomicAdd(&b.mass[i], exp_near_zero((fy - fb - 0.5) * (1.0 / (TP_Y_PER_X * FINE_PER_COARSE))));
           atomicAdd(&b.cnt[i], 1u);
         }
-        if (b_lo > 0) pick_group<false>(g, x, bits, tp, p.rng, sub, excluded, keep_before, best, bar, nullptr);
-      }, share_bar);
+        if (b_lo > 0) candidates(g, x, bits, keep_before);
+      }, end_round);
       __syncthreads();
       // The fine prefix, after the mass before the coarse range, in thread order.
       const double fdM = (dM + 1.0) * (1.0 / TP_Y_PER_X);
@@ -1991,16 +2114,19 @@ template <int DT, bool VEC> struct FullRow {
         if (k < double(b_lo) || k > double(b_hi)) return false;
         return fine_top - floor(double(v) * inv4 * FINE_PER_COARSE) < fine_from;
       };
+      round_base = tid;
       each_group([&](int g, const W (&x)[4], uint32_t bits) {
         gather_group(g, x, bits);
-        pick_group<false>(g, x, bits, tp, p.rng, sub, excluded, keep_fine, best, bar, nullptr);
-      }, share_bar);
+        candidates(g, x, bits, keep_fine);
+      }, end_round);
     } else {
       each_group([&](int g, const W (&x)[4], uint32_t bits) {
         gather_group(g, x, bits);
-        if (b_lo > 0) pick_group<false>(g, x, bits, tp, p.rng, sub, excluded, keep_before, best, bar, nullptr);
-      }, share_bar);
+        if (b_lo > 0) candidates(g, x, bits, keep_before);
+      }, end_round);
     }
+    dp.drain(b.pq, p.rng, sub, true, xs_of);
+    Pick best = dp.best;
     __syncthreads();
     const int n = b.n;
     if (n == 0 || n > GATHER_CAP) return false;
