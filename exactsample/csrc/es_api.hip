@@ -1,6 +1,7 @@
 // Host side of exactsample_amd: launch geometry, dtype dispatch and the C ABI
 // (include/exactsample_amd.h).
 #include <limits.h>
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 #include <stdio.h>
@@ -9,6 +10,7 @@
 
 namespace {
 constexpr int kBlock = 256;  // threads per block of the kernel
+constexpr int64_t kFinishSlots = 512;  // es_finish blocks resident at once on MI355X: 256 CUs x 2
 thread_local char g_last_hip_error[256] = "";
 thread_local hipEvent_t g_split_event = nullptr;
 std::atomic<uint32_t> g_generation{0};
@@ -150,6 +152,15 @@ int32_t launch_call(const es_arguments& a, void* stream_ptr, bool own_workspace)
   const int cap_total = a.target.dtype == ES_F64 ? es::cand_capacity<double>() : es::cand_capacity<float>();
   pl.cap_slice = cap_total / pl.slices;
   pl.slice_blocks = int(a.rows * pl.slices);
+  // A binned top-p row (list rows only) has its boundary pass shared by
+  // `parts` finishing blocks, each taking whole slices; the blocks of other
+  // rows exit at once. About one round of the device's resident finishing
+  // blocks (two per CU) for the call, at least two per row.
+  pl.helpers = 0;
+  if (run.list_max > 0 && pl.tiles == 1 && pl.slices > 1 && pl.slices <= es::TP_SLICES_MAX) {
+    const int64_t parts = std::min<int64_t>(pl.slices, std::max<int64_t>(2, (kFinishSlots + a.rows - 1) / a.rows));
+    pl.helpers = int(parts - 1);
+  }
   pl.generation = next_generation();
   hipError_t err = hipSuccess;
   switch (a.target.dtype) {

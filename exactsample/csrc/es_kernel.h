@@ -54,13 +54,10 @@ constexpr int HEAD_BINS = 256;            // quarter-logit bins below the maximu
 constexpr int TOPP_HEAD = 96;             // entries a top-p list sorts first
 // Binned top-p rows: each slice bins its kept tokens on the grid y = l * 4 / T
 // (bin b holds y in [b, b + 1), a quarter of a unit of x = (l - max) / T), in
-// the 64 bins below its reference maximum: per bin the count and the sum of
-// e^((y - b - 1/2) / 4), i.e. the weights relative to the bin's centre. The
-// grid is absolute, so the slices' bins merge by addition.
-constexpr int TP_COARSE = 64;
+// the TP_COARSE bins below its reference maximum: per bin the count and the
+// sum of e^((y - b - 1/2) / 4), i.e. the weights relative to the bin's centre.
+// The grid is absolute, so the slices' bins merge by addition.
 constexpr double TP_Y_PER_X = 4.0;
-constexpr size_t TP_SLICE_BIN_BYTES = TP_COARSE * (sizeof(double) + sizeof(uint16_t));
-constexpr int TP_SLICES_MAX = int(CAND_BYTES / TP_SLICE_BIN_BYTES);
 
 // ---------------------------------------------------------------------------
 // Element types.
@@ -155,10 +152,21 @@ struct Pick;
 template <class W> __device__ __forceinline__ Pick* slice_pick(const es_arguments& a, int64_t row, int slice, int cap) {
   return reinterpret_cast<Pick*>(candidates<W>(a, row) + int64_t(slice) * cap);
 }
-// A binned top-p row's slice keeps its bins where a list row keeps candidates:
+// A binned top-p row's slice keeps its bins at the end of the row region:
 // TP_COARSE FP64 masses, then TP_COARSE 16-bit counts.
 __device__ __forceinline__ double* slice_bin_mass(const es_arguments& a, int64_t row, int slice) {
-  return reinterpret_cast<double*>(row_region(a, row) + OFF_CAND + size_t(slice) * TP_SLICE_BIN_BYTES);
+  return reinterpret_cast<double*>(row_region(a, row) + ROW_BYTES - size_t(slice + 1) * TP_SLICE_BIN_BYTES);
+}
+// The boundary area of a binned top-p row of `slices` slices: the gathered
+// count, the finishing blocks' picks and the gathered IDs (or the bitmap).
+__device__ __forceinline__ uint32_t* bound_count(const es_arguments& a, int64_t row, int slices) {
+  return reinterpret_cast<uint32_t*>(row_region(a, row) + bound_area_offset(slices));
+}
+__device__ __forceinline__ uint32_t* bound_picks(const es_arguments& a, int64_t row, int slices) {
+  return bound_count(a, row, slices) + 2;
+}
+__device__ __forceinline__ uint32_t* bound_ids(const es_arguments& a, int64_t row, int slices) {
+  return bound_picks(a, row, slices) + slices * int(TP_PICK_BYTES / 4);
 }
 __device__ __forceinline__ uint16_t* slice_bin_count(const es_arguments& a, int64_t row, int slice) {
   return reinterpret_cast<uint16_t*>(slice_bin_mass(a, row, slice) + TP_COARSE);
@@ -1331,6 +1339,9 @@ __device__ __forceinline__ Pick range_pick(const es_arguments& a, int64_t row, c
 // is monotone in l. A dense boundary bin is split 64 ways on the finer grid
 // floor(64 y), which nests in it.
 constexpr int TP_BINS = 1024;  // fine bins of the boundary's coarse range, at most
+constexpr int TP_GATHER_MAX = 2048;  // gathered tokens of the boundary's bins, at most (4-byte logits)
+template <class W> constexpr int tp_gather_cap() { return sizeof(W) == 4 ? TP_GATHER_MAX : TP_GATHER_MAX / 2; }
+constexpr int TP_FINE = 64;  // fine bins per coarse bin (y * 64 on the same grid)
 constexpr int TP_SCALARS = 16;
 
 // e^d for |d| <= 1/8: the Taylor polynomial through d^11 (truncation below
@@ -1366,15 +1377,18 @@ __device__ __forceinline__ double exp_near_zero(double d) {
 // The row's bins (es_finish only; the gathered tokens of the boundary bins
 // live in the block's list union).
 // A wave's queue of groups whose tokens may win a Gumbel-max draw, drained
-// 64 at a time with one group per lane (see DensePick).
-constexpr int PQ_CAP = 128;
+// 64 at a time with one group per lane (see DensePick): room for a round of
+// PQ_ROUND offers per lane on top of 63 left from the last drain.
+constexpr int PQ_ROUND = 8;
+constexpr int PQ_CAP = WAVE * (PQ_ROUND + 1);
 struct PickQueue {
   int g[WAVES][PQ_CAP];          // group
   uint32_t live[WAVES][PQ_CAP];  // its candidates (bit j: token 4 g + j)
 };
 
 struct TopPBins {
-  double mass[TP_BINS];   // sum over the bin's kept tokens of their weights relative to the bin's centre
+  double mass[TP_GATHER_MAX];  // fine bins: sum over the bin's kept tokens of their weights relative to
+                              // the bin's centre; later the gathered tokens' FP64 weights
   unsigned cnt[TP_BINS];  // kept tokens in the bin
   double scal[TP_SCALARS];
   int n;                  // tokens gathered
@@ -1412,19 +1426,25 @@ struct DensePick {
     }
     n += __popcll(has);
   }
-  // Draws queued groups once 64 are waiting (or all of them with `all`);
-  // xs_of(g, xs) gives the FP32 x of group g's four tokens.
-  template <class XsOf>
-  __device__ __forceinline__ void drain(PickQueue& q, const RngAddr& rng, uint32_t sub, bool all, XsOf&& xs_of) {
+  // Draws queued groups once 64 are waiting (or all of them with `all`):
+  // prep(g, queued, xs) gives the FP32 x of group g's four tokens and returns
+  // the tokens to draw, a subset of those queued (it may act on the others).
+  template <class Prep>
+  __device__ __forceinline__ void drain(PickQueue& q, const RngAddr& rng, uint32_t sub, bool all, Prep&& prep) {
     const int w = wave_id(), lane = lane_id();
     while (n >= WAVE || (all && n > 0)) {
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      const int take = min(n, WAVE);
+      // The last `take` entries, one per lane (the order of draws does not
+      // change the pick).
+      const int take = min(n, WAVE), from = n - take;
+      float xs[4];
+      uint32_t live = 0;
+      int g = 0;
       if (lane < take) {
-        const int g = q.g[w][lane];
-        const uint32_t live = q.live[w][lane];
-        float xs[4];
-        xs_of(g, xs);
+        g = q.g[w][from + lane];
+        live = prep(g, q.live[w][from + lane], xs);
+      }
+      if (live) {
         const Words w4 = philox(rng.seed, rng.stream, rng.position, sub, uint32_t(g));
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -1447,21 +1467,9 @@ struct DensePick {
           bar = fmaxf(bar, best.lo - PRUNE_MARGIN);
         }
       }
-      // Move the rest to the front (at most 63 entries) and share the bar.
+      // Share the bar; later offers reuse the entries drawn.
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      const int rest = n - take;
-      int g2 = 0;
-      uint32_t l2 = 0;
-      if (lane < rest) {
-        g2 = q.g[w][take + lane];
-        l2 = q.live[w][take + lane];
-      }
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      if (lane < rest) {
-        q.g[w][lane] = g2;
-        q.live[w][lane] = l2;
-      }
-      n = rest;
+      n = from;
       bar = fmaxf(bar, wave_all(best.lo, [](float u, float v) { return u > v ? u : v; }, -INFINITY) - PRUNE_MARGIN);
     }
   }
@@ -1805,9 +1813,9 @@ template <int DT, bool VEC> struct FullRow {
     Pick pick;              // certified pick of draw `sub` over the nucleus
   };
   using GKey = typename std::conditional<sizeof(W) == 4, uint64_t, u128>::type;
-  static constexpr int GATHER_CAP = 1024;
-  static constexpr int FINE_PER_COARSE = 64;  // fine bins: y * 64 on the same grid
-  static_assert(GATHER_CAP * (sizeof(GKey) + sizeof(double)) <= sizeof(Shared<W>::u), "gathered tokens fit the union");
+  static constexpr int GATHER_CAP = tp_gather_cap<W>();
+  static constexpr int FINE_PER_COARSE = TP_FINE;
+  static_assert(GATHER_CAP * sizeof(GKey) <= sizeof(Shared<W>::u), "gathered keys fit the union");
 
   __device__ __forceinline__ GKey gkey(W v, int t) const { return GKey(CK<W>::make(v, t)); }
   __device__ __forceinline__ W gvalue(GKey k) const { return CK<W>::value(u128(k)); }
@@ -1850,15 +1858,131 @@ template <int DT, bool VEC> struct FullRow {
     }
   }
 
+  // One pass over groups [g_begin, g_end), PQ_ROUND groups in flight per
+  // thread: a group holding a valid token with x32 >= lowest is queued on
+  // dp (those tokens' bits), and classify(g, queued, xs) settles the queued
+  // tokens as dp draws them (see DensePick::drain). Every thread calls it.
+  template <class C>
+  __device__ __forceinline__ void queue_pass(int g_begin, int g_end, float lowest, DensePick& dp, uint32_t sub,
+                                             C&& classify) {
+    PickQueue& q = tb->pq;
+    for (int base0 = g_begin; base0 < g_end; base0 += BLOCK * PQ_ROUND) {  // a uniform trip count: dp's queue is per wave
+      const int base = base0 + int(threadIdx.x);
+      W x[PQ_ROUND][4];
+      uint32_t bits[PQ_ROUND];
+#pragma unroll
+      for (int u = 0; u < PQ_ROUND; ++u) {
+        const int g = base + u * BLOCK;
+        view.load(min(g, g_end - 1), x[u]);
+        bits[u] = g < g_end ? group_bits(a, row, g) : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < PQ_ROUND; ++u) {
+        uint32_t queued = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const W v = x[u][j];
+          if (((bits[u] >> j) & 1u) && v > neg_inf<W>() && tp.x32(v) >= lowest) queued |= 1u << j;
+        }
+        dp.offer(q, base + u * BLOCK, queued);
+      }
+      dp.drain(q, p.rng, sub, false, classify);
+    }
+    dp.drain(q, p.rng, sub, true, classify);
+  }
+
+  // A pass over the runs of TP_RUN tokens marked in `bitmap` (words [0,
+  // nwords)): BLOCK words at a time, the marked runs are listed in LDS (the
+  // upper part of the bins' mass array, free in the dense passes; in batches
+  // of TP_RUN_LIST), then their groups are queued on dp as in queue_pass,
+  // PQ_ROUND groups per thread per round. Every thread calls it.
+  static constexpr int TP_RUN_LIST = TP_GATHER_MAX * 2 - TP_BINS * 2;  // 32-bit entries past the fine bins
+  template <class C>
+  __device__ __forceinline__ void guided_pass(const uint32_t* bitmap, int nwords, float lowest, DensePick& dp,
+                                              uint32_t sub, C&& classify) {
+    PickQueue& q = tb->pq;
+    uint32_t* list = reinterpret_cast<uint32_t*>(tb->mass + TP_BINS);
+    constexpr int GPR = TP_RUN / 4;          // groups per run
+    constexpr int RPT = PQ_ROUND / GPR;      // runs per thread per round
+    const int tid = threadIdx.x, lane = lane_id(), wid = wave_id();
+    for (int w0 = 0; w0 < nwords; w0 += BLOCK) {  // uniform trip counts throughout: dp's queue is per wave
+      const int wi = w0 + tid;
+      const uint32_t word = wi < nwords ? bitmap[wi] : 0u;
+      const int cnt = int(__popc(word));
+      const int incl = wave_scan(cnt, [](int x, int y) { return x + y; }, 0);
+      __syncthreads();
+      if (lane == WAVE - 1) sh.ired[wid] = incl;
+      __syncthreads();
+      int first = incl - cnt, total = 0;
+      for (int w = 0; w < WAVES; ++w) {
+        if (w < wid) first += sh.ired[w];
+        total += sh.ired[w];
+      }
+      for (int k0 = 0; k0 < total; k0 += TP_RUN_LIST) {
+        __syncthreads();  // the list's last batch is read
+        uint32_t wd = word;
+        for (int idx = first; wd; ++idx) {
+          const int bit = __ffs(wd) - 1;
+          wd &= wd - 1;
+          if (idx >= k0 && idx < k0 + TP_RUN_LIST) list[idx - k0] = uint32_t(32 * wi + bit);
+        }
+        __syncthreads();
+        const int n = min(TP_RUN_LIST, total - k0);
+        for (int r0 = 0; r0 < n; r0 += BLOCK * RPT) {
+          W x[RPT * GPR][4];
+          uint32_t bits[RPT * GPR];
+          int gs[RPT * GPR];
+#pragma unroll
+          for (int u = 0; u < RPT; ++u) {
+            const int li = r0 + tid + u * BLOCK;
+            const int run = li < n ? int(list[li]) : -1;
+#pragma unroll
+            for (int h = 0; h < GPR; ++h) {
+              const int g = run * GPR + h, i = u * GPR + h;
+              gs[i] = run >= 0 && g < groups ? g : -1;
+              view.load(gs[i] >= 0 ? g : 0, x[i]);
+              bits[i] = gs[i] >= 0 ? group_bits(a, row, g) : 0u;
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < RPT * GPR; ++i) {
+            uint32_t queued = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              if (((bits[i] >> j) & 1u) && x[i][j] > neg_inf<W>() && tp.x32(x[i][j]) >= lowest) queued |= 1u << j;
+            }
+            dp.offer(q, gs[i], queued);
+          }
+          dp.drain(q, p.rng, sub, false, classify);
+        }
+      }
+    }
+    dp.drain(q, p.rng, sub, true, classify);
+  }
+
   int bin_slices = 0;  // > 0: the row's slices binned its kept weights
+  // This block's share of a binned top-p row's boundary pass: groups
+  // [part gps, (part + 1) gps) of the row's `parts` finishing blocks
+  // (parts > 1), or the whole row (parts 1).
+  int part = 0, parts = 1, gps = 0;
+  // Whether this block finishes the row: after a shared pass the last block
+  // to arrive; when the pass is not shared, the row's first block alone.
+  bool finisher = true;
 
   __device__ __forceinline__ bool topp_binned(uint32_t sub, int excluded, int floor_id, BinnedCut* out) {
-    if (!bin_slices || !tb || tp.slow) return false;
+    // Before the arrival every finishing block of the row takes the same
+    // decisions from the same data: when the pass is not shared (or cannot
+    // settle the row) the first block goes on alone and the others leave.
+    auto bail = [&]() {
+      finisher = part == 0;
+      return false;
+    };
+    if (!bin_slices || !tb || tp.slow) return bail();
     TopPBins& b = *tb;
     const int tid = threadIdx.x, lane = lane_id(), wid = wave_id();
     const double inv_t = 1.0 / p.temperature, inv4 = TP_Y_PER_X / p.temperature;
     const double M = tp.M, yM = M * inv4;
-    if (!(fabs(yM) < 0x1p50)) return false;
+    if (!(fabs(yM) < 0x1p50)) return bail();
     const double top = floor(yM), dM = top - yM;  // dM in (-1, 0]
     // A mass's relative error besides its adds: the polynomial, y's formation
     // (|y| 2^-53 per token and for dM) and the FP64 exp of the bin factor.
@@ -1866,43 +1990,64 @@ template <int DT, bool VEC> struct FullRow {
     auto coarse_of = [&](W v) -> double { return top - floor(double(v) * inv4); };
     // The x of the lower edge of row bin k (bin top - k holds y in [top - k, top - k + 1)).
     auto coarse_edge = [&](double k) -> float { return float((dM - k) * (1.0 / TP_Y_PER_X)); };
-    // ---- 1. The row's bins. ----
-    if (tid < TP_COARSE) { b.mass[tid] = 0; b.cnt[tid] = 0; }
+    // ---- 1. The row's bins: one wave merges the slices' bins in slice order
+    // after loading them all, so every finishing block gets the same bits;
+    // lane k holds row bin k. The bins past the row's TP_COARSE and the
+    // slices' FP32 far parts make the far mass. From certified prefix bounds
+    // against top_p times the total: the bins [b_lo, b_hi] that may hold the
+    // boundary (reference.py:73-83) and the mass before and outside them. ----
     if (tid == 0) b.n = 0;
-    __syncthreads();
-    double fp = 0, fpe = 0;  // mass past the row's bins and its bound (FP64)
-    for (int idx = tid; idx < bin_slices * TP_COARSE; idx += BLOCK) {
-      const int sl = idx / TP_COARSE, j = idx - sl * TP_COARSE;
-      const unsigned c = slice_bin_count(a, row, sl)[j];
-      if (!c) continue;
-      const double m = slice_bin_mass(a, row, sl)[j];
-      const double k = double(j) + (top - slice_parts(a, row)[sl].frontier);
-      if (k < double(TP_COARSE)) {
-        atomicAdd(&b.mass[int(k)], m);
-        atomicAdd(&b.cnt[int(k)], c);
-      } else {
-        const double f = exp((dM + 0.5 - k) * (1.0 / TP_Y_PER_X)) * m;
-        fp += f;
-        fpe += f * (rel + double(c) * 0x1p-52);
-      }
-    }
-    if (tid < bin_slices) {  // the slices' FP32 far parts, from their reference maximum to the row's
-      const SlicePart q = slice_parts(a, row)[tid];
-      const double sh_x = (q.tau - M) * inv_t;
-      const double sc = exp(sh_x);
-      fp += q.sum * sc;
-      fpe += (q.err + 1e-15 * q.sum) * sc * (1 + 1e-13) + q.sum * sc * (fabs(sh_x) * 0x1p-50 + 1e-15);
-    }
-    const double fp_all = block_all(fp, [](double x, double y) { return x + y; }, sh.dred, 0.0);
-    const double fpe_all = block_all(fpe, [](double x, double y) { return x + y; }, sh.dred, 0.0) + 0x1p-44 * fp_all;
-    // One wave: lane k holds row bin k. Certified inclusive prefix sums, the
-    // bins that may hold the boundary and the mass outside them.
     if (wid == 0) {
-      const double f = exp((dM + 0.5 - double(lane)) * (1.0 / TP_Y_PER_X));
-      const double m = f * b.mass[lane];
-      const double e = m * (rel + double(b.cnt[lane]) * 0x1p-52);
+      double fr = -INFINITY, tau = 0, psum = 0, perr = 0;
+      if (lane < bin_slices) {
+        const SlicePart q = slice_parts(a, row)[lane];
+        fr = q.frontier; tau = q.tau; psum = q.sum; perr = q.err;
+      }
+      double ms[TP_SLICES_MAX];
+      unsigned cs[TP_SLICES_MAX];
+#pragma unroll
+      for (int sl = 0; sl < TP_SLICES_MAX; ++sl) {
+        ms[sl] = 0;
+        cs[sl] = 0;
+        if (sl < bin_slices) {
+          ms[sl] = slice_bin_mass(a, row, sl)[lane];
+          cs[sl] = slice_bin_count(a, row, sl)[lane];
+        }
+      }
+      double m = 0, fp = 0, fpe = 0;  // row bin `lane`; mass past the row's bins and its bound
+      unsigned c = 0;
+      bool off_grid = false;
+#pragma unroll
+      for (int sl = 0; sl < TP_SLICES_MAX; ++sl) {
+        const double d = sl < bin_slices ? top - lane_read(fr, sl) : double(TP_COARSE);  // slice bin j is row bin j + d
+        off_grid |= !(d >= 0);
+        const double k = double(lane) + d;
+        if (sl < bin_slices && !(k < double(TP_COARSE)) && cs[sl]) {
+          const double f = exp((dM + 0.5 - k) * (1.0 / TP_Y_PER_X)) * ms[sl];
+          fp += f;
+          fpe += f * (rel + double(cs[sl]) * 0x1p-52);
+        }
+        const int src = d < double(TP_COARSE) && d >= 0 ? lane - int(d) : -1;
+        const double mv = __shfl(ms[sl], src < 0 ? 0 : src);
+        const unsigned cv = __shfl(cs[sl], src < 0 ? 0 : src);
+        if (src >= 0) {
+          m += mv;
+          c += cv;
+        }
+      }
+      if (lane < bin_slices) {  // the slices' FP32 far parts, from their reference maximum to the row's
+        const double sh_x = (tau - M) * inv_t;
+        const double sc = exp(sh_x);
+        fp += psum * sc;
+        fpe += (perr + 1e-15 * psum) * sc * (1 + 1e-13) + psum * sc * (fabs(sh_x) * 0x1p-50 + 1e-15);
+      }
+      const double fp_all = wave_all(fp, [](double x, double y) { return x + y; }, 0.0);
+      const double fpe_all = wave_all(fpe, [](double x, double y) { return x + y; }, 0.0) + 0x1p-44 * fp_all;
+      const double mm = exp((dM + 0.5 - double(lane)) * (1.0 / TP_Y_PER_X)) * m;
+      const double e = mm * (rel + double(c) * 0x1p-52);
       struct ME { double m, e; };
-      const ME inc = wave_scan(ME{m, e}, [](ME x, ME y) { return ME{x.m + y.m, x.e + y.e}; }, ME{0, 0});
+      auto add = [](ME x, ME y) { return ME{x.m + y.m, x.e + y.e}; };
+      const ME inc = wave_scan(ME{mm, e}, add, ME{0, 0});
       const ME tot = lane_read(inc, WAVE - 1);
       const double slack = inc.e + 0x1p-44 * inc.m, tslack = tot.e + 0x1p-44 * tot.m;
       const double s_lo = tot.m - tslack + fp_all - fpe_all, s_hi = tot.m + tslack + fp_all + fpe_all;
@@ -1911,10 +2056,10 @@ template <int DT, bool VEC> struct FullRow {
       const uint64_t sure = __ballot(inc.m - slack >= hi_t);
       const int b_lo = may ? __ffsll((unsigned long long)may) - 1 : TP_COARSE;
       const int b_hi = sure ? __ffsll((unsigned long long)sure) - 1 : TP_COARSE;
-      const int count = wave_all(lane >= b_lo && lane <= b_hi ? int(b.cnt[lane]) : 0, [](int x, int y) { return x + y; }, 0);
-      // Mass before b_lo and after b_hi (inside the bins), each with its bound.
-      const ME before = wave_all(lane < b_lo ? ME{m, e} : ME{0, 0}, [](ME x, ME y) { return ME{x.m + y.m, x.e + y.e}; }, ME{0, 0});
-      const ME after = wave_all(lane > b_hi ? ME{m, e} : ME{0, 0}, [](ME x, ME y) { return ME{x.m + y.m, x.e + y.e}; }, ME{0, 0});
+      const int count = wave_all(lane >= b_lo && lane <= b_hi ? int(c) : 0, [](int x, int y) { return x + y; }, 0);
+      const ME before = wave_all(lane < b_lo ? ME{mm, e} : ME{0, 0}, add, ME{0, 0});
+      const ME after = wave_all(lane > b_hi ? ME{mm, e} : ME{0, 0}, add, ME{0, 0});
+      const bool bad_grid = __ballot(off_grid) != 0;
       if (lane == 0) {
         b.scal[0] = b_lo; b.scal[1] = b_hi; b.scal[2] = count;
         b.scal[3] = lo_t; b.scal[4] = hi_t;
@@ -1923,6 +2068,7 @@ template <int DT, bool VEC> struct FullRow {
         // Everything outside [b_lo, b_hi]: the bins before and after, and the far tail.
         b.scal[7] = fmax(before.m - be + after.m - ae + fp_all - fpe_all, 0.0);
         b.scal[8] = before.m + be + after.m + ae + fp_all + fpe_all;
+        b.scal[9] = bad_grid;
       }
     }
     __syncthreads();
@@ -1930,30 +2076,22 @@ template <int DT, bool VEC> struct FullRow {
     double lo_t = b.scal[3], hi_t = b.scal[4];
     double eb_lo = b.scal[5], eb_hi = b.scal[6];
     const double rest_lo = b.scal[7], rest_hi = b.scal[8];
+    const bool bad_grid = b.scal[9] != 0;
     __syncthreads();
-    if (b_hi >= TP_COARSE || b_lo > b_hi || count == 0) return false;  // the boundary may lie in the far tail
-    // ---- 2. Gather the boundary's tokens; pick over the ones before them. ----
+    // The boundary may lie in the far tail (or a slice's grid is off the row's).
+    if (bad_grid || b_hi >= TP_COARSE || b_lo > b_hi || count == 0) return bail();
+    // ---- 2. This block's share of the pass: the tokens of [b_lo, b_hi]
+    // gathered (unless more than the list holds: dense), and the pick over
+    // the tokens before them. A shared pass gathers token IDs into the row's
+    // boundary area; a lone block gathers keys into its list. ----
     GKey* keys = reinterpret_cast<GKey*>(&sh.u);
-    double* wts = reinterpret_cast<double*>(keys + GATHER_CAP);
+    double* wts = b.mass;  // the gathered weights, once the fine bins are done with
+    const bool shared_pass = parts > 1;
+    const int gcap = shared_pass ? min(GATHER_CAP, bound_capacity(bin_slices)) : GATHER_CAP;
+    const bool dense = count > gcap;
     const float edge_before = coarse_edge(double(b_lo) - 1.0);  // x at or above it: coarse bin < b_lo
     const float edge_range = coarse_edge(double(b_hi));          // x below it: coarse bin > b_hi
     constexpr float SCREEN = 1e-5f;  // above x32's error for |x| <= 17
-    // Tokens before the gathered range are certainly kept (their bin lies
-    // before the boundary's); the range's lower end in fine bins, if any.
-    double fine_top = 0;  // fine index of a token: fine_top - floor(y * 64)
-    int f_lo = -1;        // >= 0: gather fine bins [f_lo, f_hi] of the coarse range
-    int f_hi = -1;
-    auto before_range = [&](W v, float x) -> bool {
-      if (x < edge_before - SCREEN) {
-        if (f_lo < 0 || x < edge_range - SCREEN) return false;
-      } else if (x > edge_before + SCREEN) {
-        return true;
-      }
-      const double k = coarse_of(v);
-      if (k < double(b_lo)) return true;
-      if (f_lo < 0 || k > double(b_hi)) return false;
-      return fine_top - floor(double(v) * inv4 * FINE_PER_COARSE) < double(f_lo);
-    };
     float floor_score = -INFINITY;
     if (floor_id >= 0 && floor_id != excluded && b_lo > 0) {
       const W v = view.value(floor_id);
@@ -1965,65 +2103,140 @@ template <int DT, bool VEC> struct FullRow {
     }
     DensePick dp;
     dp.init(floor_score);
-    auto xs_of = [&](int g, float (&xs)[4]) {
-      W v[4];
-      view.load(g, v);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) xs[j] = tp.x32(v[j]);
-    };
-    // The streaming loop records each group's candidates (tokens where
-    // keep(v, x) holds, the draft left out) in round_cand, 4 bits per group
-    // of the round; after the round the groups are queued for the draw.
-    uint64_t round_cand = 0;
-    int round_base = tid;  // the first group of the current round for this thread
-    auto candidates = [&](int g, const W (&x)[4], uint32_t bits, auto&& keep) {
-      uint32_t cand = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const W v = x[j];
-        if (((bits >> j) & 1u) && v > neg_inf<W>() && 4 * g + j != excluded && keep(v, tp.x32(v))) cand |= 1u << j;
-      }
-      const int u = (g - round_base) / BLOCK;  // the group's place in the round
-      round_cand |= uint64_t(cand) << (4 * u);
-    };
-    auto end_round = [&]() {
-      for (int u = 0; u < TGP; ++u) {
-        dp.offer(b.pq, round_base + u * BLOCK, uint32_t(round_cand >> (4 * u)) & 0xfu);
-        dp.drain(b.pq, p.rng, sub, false, xs_of);
-      }
-      round_cand = 0;
-      round_base += BLOCK * TGP;
-    };
-    auto keep_before = [&](W v, float x) { return tp.kept(v, x) && before_range(v, x); };
-    const bool dense = count > GATHER_CAP;
-    if (dense) {
-      // The coarse range binned 64 times finer (y * 64 on the same grid):
-      // fine bin f of coarse bin k is 64 k + (63 - (floor(64 y) - 64 floor(y))).
-      fine_top = (top + 1) * FINE_PER_COARSE - 1;
-      const int nfine = (b_hi - b_lo + 1) * FINE_PER_COARSE;
-      if (nfine > TP_BINS) return false;
+    uint32_t* const gcount = bound_count(a, row, bin_slices);  // the area's layout follows the slices
+    uint32_t* const gids = bound_ids(a, row, bin_slices);
+    // A dense range is binned 64 times finer (y * 64 on the same grid: fine
+    // bin f of coarse bin k is 64 k + (63 - (floor(64 y) - 64 floor(y)))):
+    // by a lone block in the same pass; after a shared pass by the finisher,
+    // which visits only the runs of TP_RUN tokens the pass marked in the
+    // boundary area's bitmap (when it fits), else the whole row.
+    const double fine_top = (top + 1) * FINE_PER_COARSE - 1;  // fine index of a token: fine_top - floor(y * 64)
+    const double fine_base = double(b_lo) * FINE_PER_COARSE;
+    const int nfine = (b_hi - b_lo + 1) * FINE_PER_COARSE;
+    if (dense && nfine > TP_BINS) return bail();
+    const int bitmap_words = int(min<int64_t>(bound_bitmap_words(a.vocab), INT_MAX));
+    const bool marks = dense && shared_pass && bitmap_words <= bound_capacity(bin_slices);
+    const bool fine_local = dense && !shared_pass;
+    if (fine_local) {
       for (int i = tid; i < nfine; i += BLOCK) { b.mass[i] = 0; b.cnt[i] = 0; }
       __syncthreads();
-      const double base = double(b_lo) * FINE_PER_COARSE;
-      each_group([&](int g, const W (&x)[4], uint32_t bits) {
+    }
+    auto fine_of = [&](W v) { return fine_top - floor(double(v) * inv4 * FINE_PER_COARSE); };
+    auto add_fine = [&](W v) {
+      const double fy = double(v) * inv4 * FINE_PER_COARSE, fb = floor(fy);
+      const int i = int(fine_top - fb - fine_base);  // in [0, nfine): the fine grid nests in the coarse one
+      if (i < 0 || i >= nfine) return;
+      atomicAdd(&b.mass[i], exp_near_zero((fy - fb - 0.5) * (1.0 / (TP_Y_PER_X * FINE_PER_COARSE))));
+      atomicAdd(&b.cnt[i], 1u);
+    };
+    // A queued group's tokens: the ones before the range drawn (the draft
+    // left out); the ones in it gathered, or for a dense range marked or
+    // binned finer.
+    auto classify = [&](int g, uint32_t queued, float (&xs)[4]) -> uint32_t {
+      W v[4];
+      view.load(g, v);
+      uint32_t draw = 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const W v = x[j];
-          if (!(((bits >> j) & 1u) && v > neg_inf<W>())) continue;
-          const float x32 = tp.x32(v);
-          if (x32 < edge_range - SCREEN || x32 > edge_before + SCREEN) continue;
-          const double k = coarse_of(v);
-          if (k < double(b_lo) || k > double(b_hi) || !tp.kept(v, x32)) continue;
-          const double fy = double(v) * inv4 * FINE_PER_COARSE, fb = floor(fy);
-          const int i = int(fine_top - fb - base);  // in [0, nfine): the fine grid nests in the coarse one
-          if (i < 0 || i >= nfine) continue;
-          atomicAdd(&b.mass[i], exp_near_zero((fy - fb - 0.5) * (1.0 / (TP_Y_PER_X * FINE_PER_COARSE))));
-          atomicAdd(&b.cnt[i], 1u);
+      for (int j = 0; j < 4; ++j) {
+        xs[j] = tp.x32(v[j]);
+        if (!((queued >> j) & 1u) || !tp.kept(v[j], xs[j])) continue;
+        const int t = 4 * g + j;
+        bool before = xs[j] > edge_before + SCREEN;
+        if (!before) {
+          const double k = coarse_of(v[j]);
+          before = k < double(b_lo);
+          if (!before && k <= double(b_hi)) {
+            if (!dense) {
+              if (shared_pass) {
+                const uint32_t slot = atomicAdd(gcount, 1u);
+                if (slot < uint32_t(gcap)) gids[slot] = uint32_t(t);
+              } else {
+                const int slot = atomicAdd(&b.n, 1);
+                if (slot < GATHER_CAP) keys[slot] = gkey(v[j], t);
+              }
+            } else if (marks) {
+              const int run = t / TP_RUN;
+              atomicOr(&gids[run >> 5], 1u << (run & 31));
+            } else if (fine_local) {
+              add_fine(v[j]);
+            }
+          }
         }
-        if (b_lo > 0) candidates(g, x, bits, keep_before);
-      }, end_round);
-      __syncthreads();
+        if (before && t != excluded) draw |= 1u << j;
+      }
+      return draw;
+    };
+    {
+      const int g_begin = shared_pass ? part * gps : 0;
+      const int g_end = shared_pass ? min(g_begin + gps, groups) : groups;
+      // Tokens below `lowest` are neither before the range nor to be gathered, marked or binned.
+      const float lowest = (dense && !marks && !fine_local ? edge_before : edge_range) - SCREEN;
+      queue_pass(g_begin, g_end, lowest, dp, sub, classify);
+    }
+    Pick best = dp.best;
+    if (shared_pass) {
+      const Pick mine = block_pick(best, sh);
+      if (tid == 0) {
+        uint32_t* rec = bound_picks(a, row, bin_slices) + part * int(TP_PICK_BYTES / 4);
+        rec[0] = __float_as_uint(mine.mid); rec[1] = __float_as_uint(mine.lo); rec[2] = __float_as_uint(mine.hi);
+        rec[3] = __float_as_uint(mine.others); rec[4] = uint32_t(mine.id);
+      }
+      if (!arrive(&counters(a, row)->bound, uint32_t(parts), &sh.flag)) {
+        finisher = false;
+        return false;
+      }
+      finisher = true;
+      // The last block: every block's pick, joined; one thread carries it on.
+      Pick theirs = pick_none();
+      if (tid < parts) {
+        const uint32_t* rec = bound_picks(a, row, bin_slices) + tid * int(TP_PICK_BYTES / 4);
+        theirs = Pick{__uint_as_float(rec[0]), __uint_as_float(rec[1]), __uint_as_float(rec[2]),
+                      __uint_as_float(rec[3]), int(rec[4])};
+      }
+      const Pick all = block_pick(theirs, sh);
+      best = tid == 0 ? all : pick_none();
+      dp.best = best;
+      dp.bar = fmaxf(dp.bar, all.lo - PRUNE_MARGIN);
+      if (!dense) {
+        const int n = int(__hip_atomic_load(gcount, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        if (n != count || n > gcap) return false;
+        for (int i = tid; i < n; i += BLOCK) {
+          const int t = int(gids[i]);
+          keys[i] = gkey(view.value(t), t);
+        }
+        if (tid == 0) b.n = n;
+      }
+    }
+    __syncthreads();
+    if (dense) {
+      // Only the coarse range's tokens matter from here on.
+      auto in_coarse = [&](W v, float x, double* k) {
+        if (x > edge_before + SCREEN || !tp.kept(v, x)) return false;
+        *k = coarse_of(v);
+        return *k >= double(b_lo) && *k <= double(b_hi);
+      };
+      if (!fine_local) {
+        // The finisher bins the coarse range finer.
+        for (int i = tid; i < nfine; i += BLOCK) { b.mass[i] = 0; b.cnt[i] = 0; }
+        __syncthreads();
+        auto bin = [&](int g, uint32_t queued, float (&xs)[4]) -> uint32_t {
+          W v[4];
+          view.load(g, v);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            xs[j] = tp.x32(v[j]);
+            double k;
+            if (((queued >> j) & 1u) && in_coarse(v[j], xs[j], &k)) add_fine(v[j]);
+          }
+          return 0u;
+        };
+        if (marks) guided_pass(gids, bitmap_words, edge_range - SCREEN, dp, sub, bin);
+        else queue_pass(0, groups, edge_range - SCREEN, dp, sub, bin);
+        __syncthreads();
+      }
       // The fine prefix, after the mass before the coarse range, in thread order.
+      const double base = fine_base;
+      int f_lo, f_hi;
       const double fdM = (dM + 1.0) * (1.0 / TP_Y_PER_X);
       double fm = 0, fe = 0;
       constexpr int PF = TP_BINS / BLOCK;
@@ -2085,48 +2298,33 @@ template <int DT, bool VEC> struct FullRow {
       if (fcount == 0 || fcount > GATHER_CAP) return false;
       f_lo += int(base);  // absolute fine indices from here on
       f_hi += int(base);
-    }
-    // The gathering pass (the second one for a dense range): the tokens of
-    // the boundary's bins, and the pick over the ones before them not picked yet.
-    const double fine_from = dense ? double(f_lo) : 0.0;
-    auto gather_group = [&](int g, const W (&x)[4], uint32_t bits) {
+      // The second dense pass, by this block alone: the tokens of fine bins
+      // [f_lo, f_hi] gathered, the coarse range's tokens before f_lo drawn
+      // (the tokens before the coarse range were drawn in the first pass).
+      auto settle = [&](int g, uint32_t queued, float (&xs)[4]) -> uint32_t {
+        W v[4];
+        view.load(g, v);
+        uint32_t draw = 0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const W v = x[j];
-        if (!(((bits >> j) & 1u) && v > neg_inf<W>())) continue;
-        const float x32 = tp.x32(v);
-        if (x32 < edge_range - SCREEN || x32 > edge_before + SCREEN) continue;
-        const double k = coarse_of(v);
-        if (k < double(b_lo) || k > double(b_hi) || !tp.kept(v, x32)) continue;
-        if (dense) {
-          const double f = fine_top - floor(double(v) * inv4 * FINE_PER_COARSE);
-          if (f < fine_from || f > double(f_hi)) continue;
+        for (int j = 0; j < 4; ++j) {
+          xs[j] = tp.x32(v[j]);
+          double k;
+          if (!((queued >> j) & 1u) || !in_coarse(v[j], xs[j], &k)) continue;
+          const double f = fine_of(v[j]);
+          const int t = 4 * g + j;
+          if (f < double(f_lo)) {
+            if (t != excluded) draw |= 1u << j;
+          } else if (f <= double(f_hi)) {
+            const int slot = atomicAdd(&b.n, 1);
+            if (slot < GATHER_CAP) keys[slot] = gkey(v[j], t);
+          }
         }
-        const int slot = atomicAdd(&b.n, 1);
-        if (slot < GATHER_CAP) keys[slot] = gkey(v, 4 * g + j);
-      }
-    };
-    if (dense) {
-      // Only the coarse range's tokens before f_lo still need the pick.
-      auto keep_fine = [&](W v, float x) {
-        if (x < edge_range - SCREEN || x > edge_before + SCREEN || !tp.kept(v, x)) return false;
-        const double k = coarse_of(v);
-        if (k < double(b_lo) || k > double(b_hi)) return false;
-        return fine_top - floor(double(v) * inv4 * FINE_PER_COARSE) < fine_from;
+        return draw;
       };
-      round_base = tid;
-      each_group([&](int g, const W (&x)[4], uint32_t bits) {
-        gather_group(g, x, bits);
-        candidates(g, x, bits, keep_fine);
-      }, end_round);
-    } else {
-      each_group([&](int g, const W (&x)[4], uint32_t bits) {
-        gather_group(g, x, bits);
-        if (b_lo > 0) candidates(g, x, bits, keep_before);
-      }, end_round);
+      if (marks) guided_pass(gids, bitmap_words, edge_range - SCREEN, dp, sub, settle);
+      else queue_pass(0, groups, edge_range - SCREEN, dp, sub, settle);
+      best = dp.best;
     }
-    dp.drain(b.pq, p.rng, sub, true, xs_of);
-    Pick best = dp.best;
     __syncthreads();
     const int n = b.n;
     if (n == 0 || n > GATHER_CAP) return false;
@@ -2433,6 +2631,7 @@ template <int DT, bool VEC> struct FullRow {
     if (p.top_p < 1 && !topk_cut && !full_q && tb) {
       binned = topp_binned(p.verify ? 2u : 0u, p.verify ? p.draft_id : -1, p.verify ? residual_floor : floor_token,
                            &bc);
+      if (!finisher) return r;  // another finishing block of the row takes it from here
       if (binned) {
         cut = bc.cut;
         den = bc.den_lo;
@@ -3417,6 +3616,19 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(5)))
   } else if (lp.binned && !bad && valid > 0) {
     // A binned top-p row: the slice's bins (n_cand TP_COARSE marks them
     // usable), its top bin in `frontier`, its reference maximum in `tau`.
+    // The first slice readies the finishing blocks' arrival counter, gathered
+    // count and, when it fits the boundary area, the bitmap.
+    if (slice == 0) {
+      if (tid == 0) {
+        counters(a, row)->bound = 0;
+        *bound_count(a, row, pl.slices) = 0;
+      }
+      const int64_t words = bound_bitmap_words(a.vocab);
+      if (words <= bound_capacity(pl.slices)) {
+        uint32_t* bitmap = bound_ids(a, row, pl.slices);
+        for (int i = tid; i < int(words); i += BLOCK) bitmap[i] = 0;
+      }
+    }
     SliceBins sb;
     if (slice_bins<DT, VEC>(a, row, slice, p, view, g0, g1, smax, pl.generation, sh, &sb)) {
       tau = sb.mref;
@@ -3525,11 +3737,16 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments, Plan) {
   __shared__ TopPBins tbins;  // the full-row path's binned top-p boundary
   const es_arguments& a = kernel_args().a;
   const Plan pl = kernel_args().pl;
-  if (int64_t(blockIdx.x) >= a.rows) {
+  // Blocks: one per row (part 0), the request blocks, then pl.helpers per row
+  // (parts 1 ... pl.helpers), which take part only in the boundary pass of a
+  // binned top-p row and otherwise leave at once.
+  const int64_t hb = int64_t(blockIdx.x) - a.rows - pl.req_blocks;
+  if (int64_t(blockIdx.x) >= a.rows && hb < 0) {
     request_block(a, int(int64_t(blockIdx.x) - a.rows));
     return;
   }
-  const int64_t row = blockIdx.x;
+  const int64_t row = hb >= 0 ? hb / pl.helpers : int64_t(blockIdx.x);
+  const int part = hb >= 0 ? 1 + int(hb - row * pl.helpers) : 0;
   const int tid = threadIdx.x;
   const int lane = lane_id();
   // One round of loads: the slices' summaries and every candidate slot wave 0
@@ -3549,18 +3766,19 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments, Plan) {
       const int idx = lane + WAVE * r;
       const int sl = map.slice(idx);
       pre[r] = Cand<W>{};
-      if (idx < pl.slices * map.pref) pre[r] = cands[sl * pl.cap_slice + (idx - sl * map.pref)];
+      if (part == 0 && idx < pl.slices * map.pref) pre[r] = cands[sl * pl.cap_slice + (idx - sl * map.pref)];
     }
   }
   const Params p = *row_meta(a, row);
-  if (tid == 0) counters(a, row)->max_key = 0;  // the slices published their maxima; ready for the next call
+  if (tid == 0 && part == 0) counters(a, row)->max_key = 0;  // the slices published their maxima; ready for the next call
   if (p.status != ES_OK || p.meta_bad) {
     // Malformed offsets or invalid request metadata: the request block reports it.
-    skip_row(a, row);
+    if (part == 0) skip_row(a, row);
     return;
   }
   const int list_max = a.list_max;
   const ListPlan lp = list_plan(p, list_max, pl.cap_slice, a.vocab, pl.slices);
+  if (part > 0 && !lp.binned) return;
   const bool sorted_list = lp.sorted_list, need_topp = lp.need_topp;
   const bool stream = a.dispatch != 1 && stream_row(p, a.vocab);  // dispatch 1: the full-row path
   const bool stream_sum = stream && stream_sub(p) == 2u;  // the ratio test needs the kept mass
@@ -3656,7 +3874,8 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments, Plan) {
   }
   __syncthreads();
   const int status = sh.bad ? ES_INVALID_INPUT : sh.valid == 0 ? ES_NO_VALID_TOKEN : ES_OK;
-  if (tid == 0) {
+  if (part > 0 && status != ES_OK) return;
+  if (tid == 0 && part == 0) {
     RowState* st = row_state(a, row);
     st->maximum = sh.maximum; st->runner_up = sh.runner_up; st->greedy = sh.greedy;
     st->runner_up_id = sh.runner_up_id; st->valid = sh.valid; st->status = status;
@@ -3707,8 +3926,13 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments, Plan) {
         int usable = 1;
         for (int sl = 0; sl < pl.slices; ++sl) usable &= sh.n_cand[sl] == TP_COARSE;
         full.bin_slices = usable ? pl.slices : 0;
+        full.parts = usable && pl.helpers > 0 ? pl.helpers + 1 : 1;
+        full.part = part;
+        full.gps = pl.gps * ((pl.slices + pl.helpers) / (pl.helpers + 1));  // whole slices per block
       }
+      if (part > 0 && full.parts == 1) return;  // only a shared boundary pass has helpers
       result = full.run(maximum, greedy, runner_up_id, valid);
+      if (!full.finisher) return;  // another of the row's blocks finishes it
       result.target_status = ES_OK;
       fallbacks += full.fallbacks;
       route = 100 + why;  // why the list could not finish it (0: not a list row)
@@ -3732,8 +3956,8 @@ hipError_t launch_main(const es_arguments& a, const Plan& pl, hipStream_t stream
   es_arguments args = a;
   Plan plan = pl;
   void* params[] = {&args, &plan};
-  // es_main: the slice blocks; es_finish: one block per row, then the
-  // request blocks.
+  // es_main: the slice blocks; es_finish: one block per row, the request
+  // blocks, then `helpers` blocks per row.
   hipError_t err = hipSuccess;
   const void* slice_kernel = pl.tiles > 1 ? reinterpret_cast<const void*>(&es_wide<DT, VEC>)
                                           : reinterpret_cast<const void*>(&es_main<DT, VEC, G>);
@@ -3742,7 +3966,8 @@ hipError_t launch_main(const es_arguments& a, const Plan& pl, hipStream_t stream
   if (err == hipSuccess && split) err = hipEventRecord(split, stream);
   if (err != hipSuccess) return err;
   return hipLaunchKernel(reinterpret_cast<const void*>(&es_finish<DT, VEC>),
-                         dim3(unsigned(a.rows + pl.req_blocks)), dim3(BLOCK), params, 0, stream);
+                         dim3(unsigned(a.rows + pl.req_blocks + a.rows * pl.helpers)), dim3(BLOCK), params, 0,
+                         stream);
 }
 
 // Contiguous rows aligned to a group of four use vector loads and, for f32

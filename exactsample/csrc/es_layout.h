@@ -53,14 +53,17 @@ static_assert(sizeof(RowState) == 48, "RowState layout");
 
 // request: rows of the request completed (an arrival counter, kept in the
 // request's first row; set to 0 by the slice pass of that row's first slice).
+// bound: a binned top-p row's finishing blocks done with their share of the
+// boundary pass (set to 0 by the row's first slice).
 // max_key: the largest slice maximum published so far in this call, as
 // (generation << 32) | FP32 order key of the maximum rounded down; min-p
 // slices read it as a lower bound on the row maximum, and a word of another
 // generation counts as nothing published.
 struct Counters {
-  uint32_t request, pad;
+  uint32_t request, bound;
   unsigned long long max_key;
 };
+static_assert(sizeof(Counters) == 16, "Counters layout");
 
 // One slice's summary of its part of the row.
 struct SlicePart {
@@ -92,4 +95,28 @@ template <class W> struct Cand { W v; int32_t id; };
 template <> struct Cand<double> { double v; int32_t id, pad; };
 template <class W> constexpr int cand_capacity() { return int(CAND_BYTES / sizeof(Cand<W>)); }
 
+// Binned top-p rows (at most TP_SLICES_MAX slices): slice s keeps TP_COARSE
+// FP64 bin masses and TP_COARSE 16-bit counts at the row region's end (its
+// bins end TP_SLICE_BIN_BYTES * s bytes before it). Between the used slice
+// parts and the bins lies the boundary area of the row's finishing blocks: a
+// 32-bit count of gathered tokens, a 32-bit pad, one 24-byte pick per
+// finishing block, then either the gathered token IDs (32-bit) or, for a
+// boundary range too dense to gather, a bitmap of the runs of TP_RUN tokens
+// that hold its tokens (bit r of word w: tokens [TP_RUN (32 w + r), + TP_RUN)).
+constexpr int TP_COARSE = 64;
+constexpr int TP_RUN = 8;
+constexpr size_t TP_SLICE_BIN_BYTES = TP_COARSE * (sizeof(double) + sizeof(uint16_t));
+constexpr int TP_SLICES_MAX = int(CAND_BYTES / TP_SLICE_BIN_BYTES);
+constexpr size_t TP_PICK_BYTES = 24;
+constexpr size_t bound_area_offset(int slices) { return OFF_PARTS + size_t(slices) * sizeof(SlicePart); }
+// 32-bit words (token IDs or bitmap words) the boundary area of a row of `slices` slices holds.
+constexpr int bound_capacity(int slices) {
+  return int((ROW_BYTES - size_t(slices) * TP_SLICE_BIN_BYTES - bound_area_offset(slices) - 8 -
+              size_t(slices) * TP_PICK_BYTES) / 4);
+}
+// Bitmap words of a vocabulary.
+constexpr int64_t bound_bitmap_words(int64_t vocab) { return (vocab + 32 * TP_RUN - 1) / (32 * TP_RUN); }
+static_assert(bound_capacity(TP_SLICES_MAX) >= 960, "the boundary area holds 960 IDs at the most slices");
+static_assert(bound_bitmap_words(int64_t(TP_SLICES_MAX) * 16 * 4 * 256) <= bound_capacity(TP_SLICES_MAX),
+              "the bitmap of the largest binned row fits the boundary area");
 }  // namespace es

@@ -18,6 +18,8 @@ struct Plan {
   int32_t cap_slice;     // candidates one slice may store
   int32_t slice_blocks;  // rows x slices: es_main's grid
   int32_t tiles;         // register tiles per slice (> 1 only for vocabularies past MAX_SLICES tiles)
+  int32_t helpers;       // es_finish blocks per row beyond the first: a binned top-p row's boundary pass,
+                         // each of the helpers + 1 blocks taking ceil(slices / (helpers + 1)) slices
   uint32_t generation;   // this call's tag for the published row maxima (never repeats on consecutive calls)
 };
 
