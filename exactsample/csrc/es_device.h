@@ -175,14 +175,16 @@ __device__ __forceinline__ float gumbel32(uint32_t w) {
                                   : -log1pf(-(float(~w) + 0.5f) * 2.3283064365386963e-10f);
   return -logf(e);
 }
-// A cheap upper bound on the same noise: -log(u) >= 1 - u, and the native
-// base-2 log with a relative margin. Checked to bound G for every word.
+// A cheap upper bound on the same noise, one native log: for w < 2^31, u <
+// 1/2, so -log(u) > log 2 and G < -log(log 2) = 0.366513 < 0.3666; otherwise
+// -log(u) >= 1 - u, with the native base-2 log and a relative margin. Checked
+// to bound G, and to stay below 23, for every word.
 __device__ __forceinline__ float gumbel_upper(uint32_t w) {
-  const float e = w < 0x80000000u ? -__logf((float(w) + 0.5f) * 2.3283064365386963e-10f)
-                                  : (float(~w) + 0.5f) * 2.3283064365386963e-10f;
+  const float e = (float(~w) + 0.5f) * 2.3283064365386963e-10f;
   const float g = -__logf(e * (1.f - 4e-6f));
-  return g + 4e-6f * (1.f + fabsf(g));
+  return w < 0x80000000u ? 0.3666f : g + 4e-6f * (1.f + fabsf(g));
 }
+constexpr float GUMBEL_UPPER_MAX = 23.f;  // gumbel_upper(w) < GUMBEL_UPPER_MAX for every word
 
 // ---------------------------------------------------------------------------
 // Temperature arithmetic and FP32 weights, with the bounds the certified
@@ -271,15 +273,20 @@ template <class W> struct Temp {
   }
   // The oracle's x = (l - max) / T in FP64 (reference.py:63).
   __device__ __forceinline__ double x64(W v) const { return (double(v) - M) / T; }
-  // FP32 x with |x32 - x| <= X_ERR_FORM * |x| + 2^-126.
-  __device__ __forceinline__ float x32(W v) const {
+  // FP32 x with |x32 - x| <= X_ERR_FORM * |x| + 2^-126; SLOW: 1 / T is out
+  // of FP32 range (`slow`), so the difference is divided in FP64. Loops that
+  // run per token choose the form once (x32_as), so no token pays for the
+  // FP64 divide.
+  template <bool SLOW> __device__ __forceinline__ float x32_as(W v) const {
     if constexpr (sizeof(W) == 8) {
       return float(x64(v));
     } else {
       const float d = v - float(M);
-      return slow ? float(double(d) / T) : d * inv_t;
+      if constexpr (SLOW) return float(double(d) / T);
+      else return d * inv_t;
     }
   }
+  __device__ __forceinline__ float x32(W v) const { return slow ? x32_as<true>(v) : x32_as<false>(v); }
   // exp(x) >= min_p and exp(x) > 0 for the FP64 x, settled in FP32 when x is
   // clear of both thresholds and in FP64 otherwise. The margin X_ERR |x| +
   // min_p_tol covers x32's formation error and ln_min_p's rounding.

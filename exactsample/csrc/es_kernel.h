@@ -1253,41 +1253,52 @@ struct KahanSum {
 // under `bar` (the floor, then the thread's best lower bound) needs no Philox
 // word; one Philox call serves the group's four tokens. With SUM, every such
 // token (the excluded one too) also goes into `sum`.
-template <bool SUM, class W, class Keep>
+template <bool SUM, bool SLOW, class W, class Keep>
 __device__ __forceinline__ void pick_group(int g, const W (&x)[4], uint32_t bits, const Temp<W>& tp,
                                            const RngAddr& rng, uint32_t sub, int excluded, Keep&& keep, Pick& best,
                                            float& bar, KahanSum* sum) {
-  float xs[4];
+  // Score bounds from xe = x + SE |x| (SE = SCORE_ERR): a token scores at
+  // most x + G + SE (1 + |x| + |G|) <= xe + UB0 before its noise is known
+  // (G < GUMBEL_MAX), and <= xe + gb + UB1 with the noise bound gb (|gb| <
+  // GUMBEL_UPPER_MAX). A token whose bound is below the bar cannot win: only
+  // its bound joins `others`. The screens use the bar as the group starts.
+  constexpr float UB0 = GUMBEL_MAX + SCORE_ERR * (1.f + GUMBEL_MAX);
+  constexpr float UB1 = SCORE_ERR * (1.f + GUMBEL_UPPER_MAX);
+  float xs[4], xe[4];
   uint32_t live = 0;
+  const float bar0 = bar - UB0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const W v = x[j];
-    xs[j] = tp.x32(v);
+    xs[j] = tp.template x32_as<SLOW>(v);
+    xe[j] = fmaf(fabsf(xs[j]), SCORE_ERR, xs[j]);
     const bool ok = ((bits >> j) & 1u) && v > neg_inf<W>() && keep(v, xs[j]);
     if constexpr (SUM) {
       if (ok) sum->add(xs[j]);
     }
-    if (!ok || 4 * g + j == excluded) continue;
-    const float ub = xs[j] + GUMBEL_MAX + SCORE_ERR * (1.f + fabsf(xs[j]) + GUMBEL_MAX);
-    if (ub < bar) {
-      best.others = fmaxf(best.others, ub);
-      continue;
-    }
-    live |= 1u << j;
+    const bool cand = ok && 4 * g + j != excluded;
+    const bool low = xe[j] < bar0;
+    best.others = fmaxf(best.others, cand && low ? xe[j] + UB0 : -INFINITY);
+    live |= cand && !low ? 1u << j : 0u;
   }
   if (!live) return;
   const Words w4 = philox(rng.seed, rng.stream, rng.position, sub, uint32_t(g));
+  const float bar1 = bar - UB1;
+  uint32_t close = 0;  // tokens whose bound reaches the bar: scored with the accurate noise
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    if (!((live >> j) & 1u)) continue;
-    const uint32_t w = w4.w[j];
-    const float gb = gumbel_upper(w);
-    const float ub2 = xs[j] + gb + SCORE_ERR * (1.f + fabsf(xs[j]) + fabsf(gb));
-    if (ub2 < bar) {
-      best.others = fmaxf(best.others, ub2);
-      continue;
-    }
-    const float G = gumbel32(w), sc = xs[j] + G, e = SCORE_ERR * (1.f + fabsf(xs[j]) + fabsf(G));
+    const float ub = xe[j] + gumbel_upper(w4.w[j]);
+    const bool on = (live >> j) & 1u;
+    const bool low = ub < bar1;
+    best.others = fmaxf(best.others, on && low ? ub + UB1 : -INFINITY);
+    close |= on && !low ? 1u << j : 0u;
+  }
+  while (close) {
+    const int j = __ffs(close) - 1;
+    close &= close - 1;
+    const uint32_t w = j == 0 ? w4.w[0] : j == 1 ? w4.w[1] : j == 2 ? w4.w[2] : w4.w[3];
+    const float xj = j == 0 ? xs[0] : j == 1 ? xs[1] : j == 2 ? xs[2] : xs[3];
+    const float G = gumbel32(w), sc = xj + G, e = SCORE_ERR * (1.f + fabsf(xj) + fabsf(G));
     const int t = 4 * g + j;
     if (sc > best.mid || (sc == best.mid && t < best.id)) {
       best.others = fmaxf(best.others, best.hi);
@@ -1302,11 +1313,11 @@ __device__ __forceinline__ void pick_group(int g, const W (&x)[4], uint32_t bits
 // The thread's certified pick over the allowed tokens of groups [g_begin,
 // g_end) read from memory, B groups in flight per thread (thread k takes
 // g_begin + k, + BLOCK, ...).
-template <int B, bool SUM, int DT, bool VEC, class Keep>
-__device__ __forceinline__ Pick range_pick(const es_arguments& a, int64_t row, const RowView<DT, VEC>& view,
-                                           int g_begin, int g_end, const Temp<typename Ty<DT>::W>& tp,
-                                           const RngAddr& rng, uint32_t sub, int excluded, float floor, Keep&& keep,
-                                           KahanSum* sum) {
+template <int B, bool SUM, bool SLOW, int DT, bool VEC, class Keep>
+__device__ __forceinline__ Pick range_pick_as(const es_arguments& a, int64_t row, const RowView<DT, VEC>& view,
+                                              int g_begin, int g_end, const Temp<typename Ty<DT>::W>& tp,
+                                              const RngAddr& rng, uint32_t sub, int excluded, float floor,
+                                              Keep&& keep, KahanSum* sum) {
   using W = typename Ty<DT>::W;
   Pick best = pick_none();
   float bar = floor - PRUNE_MARGIN;
@@ -1325,11 +1336,21 @@ __device__ __forceinline__ Pick range_pick(const es_arguments& a, int64_t row, c
       mb[u] = g < g_end ? group_bits(a, row, g) : 0u;
     }
 #pragma unroll
-    for (int u = 0; u < B; ++u) pick_group<SUM>(base + u * BLOCK, x[u], mb[u], tp, rng, sub, excluded, keep, best, bar, sum);
+    for (int u = 0; u < B; ++u)
+      pick_group<SUM, SLOW>(base + u * BLOCK, x[u], mb[u], tp, rng, sub, excluded, keep, best, bar, sum);
     const float wave_lo = wave_all(best.lo, [](float p, float q) { return p > q ? p : q; }, -INFINITY);
     bar = fmaxf(bar, wave_lo - PRUNE_MARGIN);
   }
   return best;
+}
+template <int B, bool SUM, int DT, bool VEC, class Keep>
+__device__ __forceinline__ Pick range_pick(const es_arguments& a, int64_t row, const RowView<DT, VEC>& view,
+                                           int g_begin, int g_end, const Temp<typename Ty<DT>::W>& tp,
+                                           const RngAddr& rng, uint32_t sub, int excluded, float floor, Keep&& keep,
+                                           KahanSum* sum) {
+  if (tp.slow)
+    return range_pick_as<B, SUM, true>(a, row, view, g_begin, g_end, tp, rng, sub, excluded, floor, keep, sum);
+  return range_pick_as<B, SUM, false>(a, row, view, g_begin, g_end, tp, rng, sub, excluded, floor, keep, sum);
 }
 
 // ---------------------------------------------------------------------------
@@ -2795,7 +2816,9 @@ __device__ __forceinline__ SliceDraw slice_draw(const es_arguments& a, int64_t r
   }
   Temp<W> ts;
   ts.init(mref, p.temperature, p.min_p);
-  auto maybe_kept = [&](W, float x) { return x > -746.5f && x >= ts.ln_min_p - (X_ERR * fabsf(x) + ts.min_p_tol); };
+  // x may be kept: x + X_ERR |x| >= ln(min_p) - tol (x32 is within X_ERR |x| of x), and no underflow.
+  const float keep_lo = ts.ln_min_p - ts.min_p_tol;
+  auto maybe_kept = [&](W, float x) { return x > -746.5f && fmaf(fabsf(x), X_ERR, x) >= keep_lo; };
   // The floor: the slice maximum's own score, when it may be drawn.
   auto floor_of = [&]() {
     if (tid == 0) {

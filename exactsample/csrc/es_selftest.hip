@@ -7,7 +7,8 @@
 // G(w) = -log(-log u), u = (w + 0.5) / 2^32. The draws assume, for every word,
 // |gumbel32(w) - G(w)| <= GUMBEL_ERR (1 + |G|), gumbel_upper(w) >= G(w) and
 // G(w) < GUMBEL_MAX (reference: tests/exhaustive/gumbel_bound.cu:1-78 makes
-// the same three checks of its CUDA noise).
+// the same three checks of its CUDA noise), and gumbel_upper(w) <
+// GUMBEL_UPPER_MAX (counted with the range violations).
 //
 // es_check_weights: the FP32 weights of the certified sums (weight32 and
 // Temp::x32 in es_device.h): every FP32 x in [-40, 0] against FP64 exp, and
@@ -53,7 +54,7 @@ __global__ void __launch_bounds__(BLOCK) check_noise(uint64_t first, uint64_t co
     lo = fmin(lo, g);
     bad_err += ratio > 1.0;
     bad_upper += margin < 0.0;
-    bad_range += !(g < double(GUMBEL_MAX));
+    bad_range += !(g < double(GUMBEL_MAX)) || !(gumbel_upper(w) < GUMBEL_UPPER_MAX);
     ++n;
   }
   const auto add = [](uint64_t x, uint64_t y) { return x + y; };
