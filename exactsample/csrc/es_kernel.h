@@ -1912,73 +1912,63 @@ template <int DT, bool VEC> struct FullRow {
     dp.drain(q, p.rng, sub, true, classify);
   }
 
-  // A pass over the runs of TP_RUN tokens marked in `bitmap` (words [0,
-  // nwords)): BLOCK words at a time, the marked runs are listed in LDS (the
-  // upper part of the bins' mass array, free in the dense passes; in batches
-  // of TP_RUN_LIST), then their groups are queued on dp as in queue_pass,
-  // PQ_ROUND groups per thread per round. Every thread calls it.
+  // The runs of TP_RUN tokens marked in `bitmap` (words [0, nwords)), listed
+  // in LDS (the upper part of the bins' mass array, free in the dense
+  // passes): returns their number, or -1 when more than TP_RUN_LIST are
+  // marked (nothing listed). Every thread calls it.
   static constexpr int TP_RUN_LIST = TP_GATHER_MAX * 2 - TP_BINS * 2;  // 32-bit entries past the fine bins
-  template <class C>
-  __device__ __forceinline__ void guided_pass(const uint32_t* bitmap, int nwords, float lowest, DensePick& dp,
-                                              uint32_t sub, C&& classify) {
-    PickQueue& q = tb->pq;
-    uint32_t* list = reinterpret_cast<uint32_t*>(tb->mass + TP_BINS);
-    constexpr int GPR = TP_RUN / 4;          // groups per run
-    constexpr int RPT = PQ_ROUND / GPR;      // runs per thread per round
+  __device__ __forceinline__ uint32_t* run_list() const { return reinterpret_cast<uint32_t*>(tb->mass + TP_BINS); }
+  __device__ __forceinline__ int list_runs(const uint32_t* bitmap, int nwords) {
     const int tid = threadIdx.x, lane = lane_id(), wid = wave_id();
-    for (int w0 = 0; w0 < nwords; w0 += BLOCK) {  // uniform trip counts throughout: dp's queue is per wave
-      const int wi = w0 + tid;
-      const uint32_t word = wi < nwords ? bitmap[wi] : 0u;
-      const int cnt = int(__popc(word));
-      const int incl = wave_scan(cnt, [](int x, int y) { return x + y; }, 0);
-      __syncthreads();
-      if (lane == WAVE - 1) sh.ired[wid] = incl;
-      __syncthreads();
-      int first = incl - cnt, total = 0;
-      for (int w = 0; w < WAVES; ++w) {
-        if (w < wid) first += sh.ired[w];
-        total += sh.ired[w];
+    const int per = (nwords + BLOCK - 1) / BLOCK;  // words per thread, consecutive
+    const int w_begin = min(nwords, tid * per), w_end = min(nwords, w_begin + per);
+    int cnt = 0;
+    for (int w = w_begin; w < w_end; ++w) cnt += int(__popc(bitmap[w]));
+    const int incl = wave_scan(cnt, [](int x, int y) { return x + y; }, 0);
+    __syncthreads();
+    if (lane == WAVE - 1) sh.ired[wid] = incl;
+    __syncthreads();
+    int idx = incl - cnt, total = 0;
+    for (int w = 0; w < WAVES; ++w) {
+      if (w < wid) idx += sh.ired[w];
+      total += sh.ired[w];
+    }
+    __syncthreads();
+    if (total > TP_RUN_LIST) return -1;
+    uint32_t* list = run_list();
+    for (int w = w_begin; w < w_end; ++w) {
+      for (uint32_t wd = bitmap[w]; wd; wd &= wd - 1) list[idx++] = uint32_t(32 * w + __ffs(wd) - 1);
+    }
+    __syncthreads();
+    return total;
+  }
+  // f(g, x, bits) on every group of the n listed runs, as loaded, four runs
+  // in flight per thread. No barrier inside.
+  template <class F> __device__ __forceinline__ void listed_pass(int n, F&& f) {
+    const uint32_t* list = run_list();
+    constexpr int GPR = TP_RUN / 4;  // groups per run
+    constexpr int RPT = 4;           // runs per thread per round
+    for (int r0 = int(threadIdx.x); r0 < n; r0 += BLOCK * RPT) {
+      W x[RPT * GPR][4];
+      uint32_t bits[RPT * GPR];
+      int gs[RPT * GPR];
+#pragma unroll
+      for (int u = 0; u < RPT; ++u) {
+        const int li = r0 + u * BLOCK;
+        const int run = li < n ? int(list[li]) : -1;
+#pragma unroll
+        for (int h = 0; h < GPR; ++h) {
+          const int g = run * GPR + h, i = u * GPR + h;
+          gs[i] = run >= 0 && g < groups ? g : -1;
+          view.load(gs[i] >= 0 ? g : 0, x[i]);
+          bits[i] = gs[i] >= 0 ? group_bits(a, row, g) : 0u;
+        }
       }
-      for (int k0 = 0; k0 < total; k0 += TP_RUN_LIST) {
-        __syncthreads();  // the list's last batch is read
-        uint32_t wd = word;
-        for (int idx = first; wd; ++idx) {
-          const int bit = __ffs(wd) - 1;
-          wd &= wd - 1;
-          if (idx >= k0 && idx < k0 + TP_RUN_LIST) list[idx - k0] = uint32_t(32 * wi + bit);
-        }
-        __syncthreads();
-        const int n = min(TP_RUN_LIST, total - k0);
-        for (int r0 = 0; r0 < n; r0 += BLOCK * RPT) {
-          W x[RPT * GPR][4];
-          uint32_t bits[RPT * GPR];
-          int gs[RPT * GPR];
-#pragma unroll
-          for (int u = 0; u < RPT; ++u) {
-            const int li = r0 + tid + u * BLOCK;
-            const int run = li < n ? int(list[li]) : -1;
-#pragma unroll
-            for (int h = 0; h < GPR; ++h) {
-              const int g = run * GPR + h, i = u * GPR + h;
-              gs[i] = run >= 0 && g < groups ? g : -1;
-              view.load(gs[i] >= 0 ? g : 0, x[i]);
-              bits[i] = gs[i] >= 0 ? group_bits(a, row, g) : 0u;
-            }
-          }
-#pragma unroll
-          for (int i = 0; i < RPT * GPR; ++i) {
-            uint32_t queued = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              if (((bits[i] >> j) & 1u) && x[i][j] > neg_inf<W>() && tp.x32(x[i][j]) >= lowest) queued |= 1u << j;
-            }
-            dp.offer(q, gs[i], queued);
-          }
-          dp.drain(q, p.rng, sub, false, classify);
-        }
+#pragma unroll 1
+      for (int i = 0; i < RPT * GPR; ++i) {
+        if (gs[i] >= 0) f(gs[i], x[i], bits[i]);
       }
     }
-    dp.drain(q, p.rng, sub, true, classify);
   }
 
   int bin_slices = 0;  // > 0: the row's slices binned its kept weights
@@ -2236,23 +2226,26 @@ template <int DT, bool VEC> struct FullRow {
         *k = coarse_of(v);
         return *k >= double(b_lo) && *k <= double(b_hi);
       };
+      auto valid_in_coarse = [&](W v, uint32_t bits, int j) {
+        double k;
+        return ((bits >> j) & 1u) && v > neg_inf<W>() && tp.x32(v) >= edge_range - SCREEN &&
+               in_coarse(v, tp.x32(v), &k);
+      };
+      // The marked runs, listed once for both passes (-1: the whole row).
+      const int listed = marks ? list_runs(gids, bitmap_words) : -1;
       if (!fine_local) {
-        // The finisher bins the coarse range finer.
+        // The finisher bins the coarse range finer: only the marked runs, or
+        // the whole row when the bitmap did not fit or marks too many.
         for (int i = tid; i < nfine; i += BLOCK) { b.mass[i] = 0; b.cnt[i] = 0; }
         __syncthreads();
-        auto bin = [&](int g, uint32_t queued, float (&xs)[4]) -> uint32_t {
-          W v[4];
-          view.load(g, v);
+        auto bin_group = [&](int, const W (&x)[4], uint32_t bits) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            xs[j] = tp.x32(v[j]);
-            double k;
-            if (((queued >> j) & 1u) && in_coarse(v[j], xs[j], &k)) add_fine(v[j]);
+            if (valid_in_coarse(x[j], bits, j)) add_fine(x[j]);
           }
-          return 0u;
         };
-        if (marks) guided_pass(gids, bitmap_words, edge_range - SCREEN, dp, sub, bin);
-        else queue_pass(0, groups, edge_range - SCREEN, dp, sub, bin);
+        if (listed >= 0) listed_pass(listed, bin_group);
+        else each_group(bin_group, [] {});
         __syncthreads();
       }
       // The fine prefix, after the mass before the coarse range, in thread order.
@@ -2322,28 +2315,26 @@ template <int DT, bool VEC> struct FullRow {
       // The second dense pass, by this block alone: the tokens of fine bins
       // [f_lo, f_hi] gathered, the coarse range's tokens before f_lo drawn
       // (the tokens before the coarse range were drawn in the first pass).
-      auto settle = [&](int g, uint32_t queued, float (&xs)[4]) -> uint32_t {
-        W v[4];
-        view.load(g, v);
+      auto settle_group = [&](int g, const W (&x)[4], uint32_t bits) {
         uint32_t draw = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          xs[j] = tp.x32(v[j]);
-          double k;
-          if (!((queued >> j) & 1u) || !in_coarse(v[j], xs[j], &k)) continue;
-          const double f = fine_of(v[j]);
+          if (!valid_in_coarse(x[j], bits, j)) continue;
+          const double f = fine_of(x[j]);
           const int t = 4 * g + j;
           if (f < double(f_lo)) {
             if (t != excluded) draw |= 1u << j;
           } else if (f <= double(f_hi)) {
             const int slot = atomicAdd(&b.n, 1);
-            if (slot < GATHER_CAP) keys[slot] = gkey(v[j], t);
+            if (slot < GATHER_CAP) keys[slot] = gkey(x[j], t);
           }
         }
-        return draw;
+        if (draw)
+          pick_group<false, false>(g, x, draw, tp, p.rng, sub, -1, [](W, float) { return true; }, dp.best, dp.bar,
+                                   nullptr);
       };
-      if (marks) guided_pass(gids, bitmap_words, edge_range - SCREEN, dp, sub, settle);
-      else queue_pass(0, groups, edge_range - SCREEN, dp, sub, settle);
+      if (listed >= 0) listed_pass(listed, settle_group);
+      else each_group(settle_group, [] {});
       best = dp.best;
     }
     __syncthreads();
