@@ -1,4 +1,4 @@
-// exactsample_amd device code: sampling and speculative-draft verification on gfx950.
+// exactsample device code: sampling and speculative-draft verification on gfx950.
 //
 // Two kernels per call (es_launch), on the caller's stream:
 //
@@ -11,19 +11,24 @@
 //  threshold chosen so that the slice's top L are stored, or exactly its first
 //  L after a radix cut (reference: fused.cuh:409-519 row_stats, :686-798
 //  row_hist/row_gather); stream rows also draw their slice's certified
-//  Gumbel-max (reference: fused.cuh:532-681 row_scan). Each slice writes a
-//  SlicePart with plain stores; the row's first slice also records the row's
-//  resolved request parameters and checks its per-row metadata.
+//  Gumbel-max (reference: fused.cuh:532-681 row_scan); binned top-p rows bin
+//  their slice's kept weights on an absolute grid (slice_bins). Each slice
+//  writes a SlicePart with plain stores; the row's first slice also records
+//  the row's resolved request parameters and checks its per-row metadata.
 //
 //  es_finish, one block per row, then ceil(R / 256) request blocks that
 //  validate each request's metadata and write the outputs of every request
-//  that fails it (reference: csrc/verify/verify.cu:6-56, initialize). A row
-//  block (the kernel boundary makes every slice's stores visible) merges the
-//  slices in slice order and finishes the row:
+//  that fails it (reference: csrc/verify/verify.cu:6-56, initialize), then
+//  Plan::helpers blocks per row that share a binned top-p row's boundary pass
+//  (and leave at once on other rows). A row block (the kernel boundary makes
+//  every slice's stores visible) merges the slices in slice order and
+//  finishes the row:
 //    - failed and greedy rows directly;
 //    - top-k rows from the union of the slices' candidates in one wave, in FP64
 //      with the oracle's formulas (reference: fused.cuh:1250-1412);
 //    - other list rows (small top-p nuclei) with the whole block;
+//    - binned top-p rows from the merged bins and one pass shared by the row's
+//      blocks, the last to arrive finishing (FullRow::topp_binned);
 //    - every other row on the full-row path, re-reading the row: exact radix
 //      cuts, exact top-p boundary, certified FP32 draws with FP64 rescoring
 //      (reference: fused.cuh:1446-1810).
@@ -1804,17 +1809,21 @@ template <int DT, bool VEC> struct FullRow {
   // ---- The binned top-p boundary ----
   // The top-p cut of a row whose slices binned its kept weights (TP_COARSE
   // bins of a quarter unit of x on the absolute grid y = l * 4 / T, see
-  // slice_bins), in one pass over the row, two when the boundary's bins are
-  // dense:
-  //  1. the slices' bins merge into the row's 64 bins below the maximum; from
-  //     certified prefix bounds against top_p times the total they give the
-  //     bins [b_lo, b_hi] that may hold the boundary (reference.py:73-83);
-  //  2. one pass gathers the tokens of [b_lo, b_hi] into the block's list
-  //     (or, past GATHER_CAP of them, bins them again 64 times finer and a
-  //     second pass gathers the fine bins that may hold the boundary), and
-  //     takes the certified FP32 Gumbel-max of draw `sub` (draft `excluded`
-  //     left out) over the tokens before them, which are certainly kept; an
-  //     FP32 screen settles most tokens with one compare;
+  // slice_bins), in one pass over the row shared by the row's `parts`
+  // finishing blocks, plus the finisher's own passes when the boundary's bins
+  // are dense:
+  //  1. each block merges the slices' bins into the row's 64 bins below the
+  //     maximum (the same bits in every block); from certified prefix bounds
+  //     against top_p times the total they give the bins [b_lo, b_hi] that
+  //     may hold the boundary (reference.py:73-83);
+  //  2. each block's part of the row: the tokens of [b_lo, b_hi] are gathered
+  //     (their IDs into the row's boundary area; a lone block gathers keys)
+  //     or, past the area's capacity, the runs holding them are marked; the
+  //     certified FP32 Gumbel-max of draw `sub` (draft `excluded` left out)
+  //     over the tokens before them, which are certainly kept, is the block's
+  //     pick. The last block to arrive finishes: for a dense range it bins the
+  //     marked runs 64 times finer and gathers the fine bins that may hold the
+  //     boundary, drawing the range's tokens before them;
   //  3. the gathered tokens are sorted (logit desc, ID asc) with their FP64
   //     weights (the oracle's formula); the boundary is the first whose
   //     double-double prefix sum plus the mass before them certainly reaches
@@ -1844,10 +1853,9 @@ template <int DT, bool VEC> struct FullRow {
   // One pass over the row, TG groups of four in flight per thread and one
   // group processed at a time (the loaded groups rotate through a fixed
   // register slot, keeping the loop body to one copy): f(g, x, bits) per
-  // group, then round() once per round, in every lane.
-  static constexpr int TGP = 16;  // groups of four in flight per thread in each_group
-  template <class F, class R> __device__ __forceinline__ void each_group(F&& f, R&& round) const {
-    constexpr int TG = TGP;
+  // group. The dense boundary's passes when no bitmap lists their runs.
+  template <class F> __device__ __forceinline__ void each_group(F&& f) const {
+    constexpr int TG = 16;
     for (int base0 = 0; base0 < groups; base0 += BLOCK * TG) {
       const int base = base0 + int(threadIdx.x);
       W x[TG][4];
@@ -1874,7 +1882,6 @@ template <int DT, bool VEC> struct FullRow {
           bits[q] = bits[q + 1];
         }
       }
-      round();
     }
   }
 
@@ -2244,7 +2251,7 @@ template <int DT, bool VEC> struct FullRow {
           }
         };
         if (listed >= 0) listed_pass(listed, bin_group);
-        else each_group(bin_group, [] {});
+        else each_group(bin_group);
         __syncthreads();
       }
       // The fine prefix, after the mass before the coarse range, in thread order.
@@ -2333,7 +2340,7 @@ template <int DT, bool VEC> struct FullRow {
                                    nullptr);
       };
       if (listed >= 0) listed_pass(listed, settle_group);
-      else each_group(settle_group, [] {});
+      else each_group(settle_group);
       best = dp.best;
     }
     __syncthreads();
