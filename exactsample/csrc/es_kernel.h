@@ -2232,11 +2232,20 @@ template <int DT, bool VEC> struct FullRow {
         *k = coarse_of(v);
         return *k >= double(b_lo) && *k <= double(b_hi);
       };
-      auto valid_in_coarse = [&](W v, uint32_t bits, int j) {
-        double k;
-        return ((bits >> j) & 1u) && v > neg_inf<W>() && tp.x32(v) >= edge_range - SCREEN &&
-               in_coarse(v, tp.x32(v), &k);
+      // The tokens of a group that may lie in the coarse range, by an FP32
+      // screen (most of a marked run does not): the FP64 tests then run only
+      // for these, one at a time per lane.
+      auto screened = [&](const W (&x)[4], uint32_t bits) {
+        uint32_t m = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float xs = tp.x32(x[j]);
+          if (((bits >> j) & 1u) && x[j] > neg_inf<W>() && xs >= edge_range - SCREEN && xs <= edge_before + SCREEN)
+            m |= 1u << j;
+        }
+        return m;
       };
+      auto pick_of = [](const W (&x)[4], int j) { return j == 0 ? x[0] : j == 1 ? x[1] : j == 2 ? x[2] : x[3]; };
       // The marked runs, listed once for both passes (-1: the whole row).
       const int listed = marks ? list_runs(gids, bitmap_words) : -1;
       if (!fine_local) {
@@ -2245,9 +2254,10 @@ template <int DT, bool VEC> struct FullRow {
         for (int i = tid; i < nfine; i += BLOCK) { b.mass[i] = 0; b.cnt[i] = 0; }
         __syncthreads();
         auto bin_group = [&](int, const W (&x)[4], uint32_t bits) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            if (valid_in_coarse(x[j], bits, j)) add_fine(x[j]);
+          for (uint32_t m = screened(x, bits); m; m &= m - 1) {
+            const W v = pick_of(x, __ffs(m) - 1);
+            double k;
+            if (in_coarse(v, tp.x32(v), &k)) add_fine(v);
           }
         };
         if (listed >= 0) listed_pass(listed, bin_group);
@@ -2323,16 +2333,18 @@ template <int DT, bool VEC> struct FullRow {
       // (the tokens before the coarse range were drawn in the first pass).
       auto settle_group = [&](int g, const W (&x)[4], uint32_t bits) {
         uint32_t draw = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (!valid_in_coarse(x[j], bits, j)) continue;
-          const double f = fine_of(x[j]);
+        for (uint32_t m = screened(x, bits); m; m &= m - 1) {
+          const int j = __ffs(m) - 1;
+          const W v = pick_of(x, j);
+          double k;
+          if (!in_coarse(v, tp.x32(v), &k)) continue;
+          const double f = fine_of(v);
           const int t = 4 * g + j;
           if (f < double(f_lo)) {
             if (t != excluded) draw |= 1u << j;
           } else if (f <= double(f_hi)) {
             const int slot = atomicAdd(&b.n, 1);
-            if (slot < GATHER_CAP) keys[slot] = gkey(x[j], t);
+            if (slot < GATHER_CAP) keys[slot] = gkey(v, t);
           }
         }
         if (draw)
