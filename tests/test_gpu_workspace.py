@@ -3,9 +3,11 @@ the op accepts runs.
 
 - Poisoning: a batch that uses every piece of per-call workspace state
   (multi-row requests and their arrival counters, min-p streaming rows and
-  their published row maxima, top-k and top-p lists, full-row rows, the
-  recompute counter) is called, every workspace byte is overwritten (0xFF,
-  then random bytes), and the next calls must return the same outputs. This
+  their published row maxima, top-k and top-p lists, binned top-p rows and
+  their boundary area (arrival counter, gathered count and IDs, or for a
+  flat row the bitmap of marked runs), full-row rows, the recompute counter)
+  is called, every workspace byte is overwritten (0xFF, then random bytes),
+  and the next calls must return the same outputs. This
   is the determinism check the reference runs under its sanitizer
   (tests/sanitizer/run.py:33-42, initcheck), made directly.
 - Vocabularies past 64 register tiles per row (f16 and f64 rows, strided
@@ -28,12 +30,14 @@ def _device(hip_device):
     load_library()
 
 
-def _mixed_batch(vocab=20000, seed=31):
+def _mixed_batch(vocab=20000, seed=31, flat=False):
     g = np.random.default_rng(seed)
     drafts = [0, 3, 0, 2, 0, 0, 1, 0]
     offsets = np.concatenate([[0], np.cumsum(np.array(drafts) + 1)])
     rows = g.normal(0.0, 2.0, size=(offsets[-1], vocab))
     rows[:, g.integers(vocab, size=12)] += 9.0
+    if flat:  # request 4 (top-p 0.8): thousands of tokens per quarter-unit bin, a dense boundary range
+        rows[offsets[4]] = g.normal(0.0, 0.3, size=vocab)
     ids = np.full((len(drafts), 3), -1)
     for r, d in enumerate(drafts):
         ids[r, :d] = np.argsort(-rows[offsets[r]])[g.integers(0, 5, size=d)]
@@ -46,11 +50,12 @@ def _mixed_batch(vocab=20000, seed=31):
     return rows, offsets, ids, params, rng
 
 
+@pytest.mark.parametrize("flat", [False, True])
 @pytest.mark.parametrize("list_max", [256, 0])
-def test_poisoned_workspace_gives_the_same_outputs(list_max):
+def test_poisoned_workspace_gives_the_same_outputs(list_max, flat):
     import torch
     from exactsample.cuda import verify
-    rows, offsets, ids, params, rng = _mixed_batch()
+    rows, offsets, ids, params, rng = _mixed_batch(flat=flat)
     out, _, args = run_and_compare(rows, offsets, ids, params=params, rng=rng, dtype=torch.float32,
                                    list_max=list_max)
     requests = len(offsets) - 1
