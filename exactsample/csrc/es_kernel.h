@@ -2857,7 +2857,13 @@ __device__ __forceinline__ SliceDraw slice_draw(const es_arguments& a, int64_t r
     out.pruned = block_all(ks.pruned, [](int x, int y) { return x + y; }, sh.ired, 0);
     pk = block_pick(pk, sh);
   } else {
-    pk = range_pick<B, false>(a, row, view, g0, g1, ts, p.rng, sub, excluded, floor_of(), maybe_kept, nullptr);
+    if (p.min_p > 0) {
+      pk = range_pick<B, false>(a, row, view, g0, g1, ts, p.rng, sub, excluded, floor_of(), maybe_kept, nullptr);
+    } else {
+      // Without min-p a token may be kept unless its weight underflows.
+      pk = range_pick<B, false>(a, row, view, g0, g1, ts, p.rng, sub, excluded, floor_of(),
+                                [](W, float x) { return x > -746.5f; }, nullptr);
+    }
     pk = block_pick(pk, sh);
     if (p.min_p > 0 && pk.id != INT_MAX) {
       const double m2 = published();
