@@ -173,6 +173,13 @@ __device__ __forceinline__ uint32_t* bound_picks(const es_arguments& a, int64_t 
 __device__ __forceinline__ uint32_t* bound_ids(const es_arguments& a, int64_t row, int slices) {
   return bound_picks(a, row, slices) + slices * int(TP_PICK_BYTES / 4);
 }
+// The shared fine bins after the bitmap: masses, then counts.
+__device__ __forceinline__ double* bound_fine_mass(const es_arguments& a, int64_t row, int slices) {
+  return reinterpret_cast<double*>(bound_ids(a, row, slices) + bound_fine_offset(a.vocab));
+}
+__device__ __forceinline__ uint32_t* bound_fine_count(const es_arguments& a, int64_t row, int slices) {
+  return reinterpret_cast<uint32_t*>(bound_fine_mass(a, row, slices) + TP_FINE_SHARED);
+}
 __device__ __forceinline__ uint16_t* slice_bin_count(const es_arguments& a, int64_t row, int slice) {
   return reinterpret_cast<uint16_t*>(slice_bin_mass(a, row, slice) + TP_COARSE);
 }
@@ -2124,9 +2131,10 @@ template <int DT, bool VEC> struct FullRow {
     uint32_t* const gids = bound_ids(a, row, bin_slices);
     // A dense range is binned 64 times finer (y * 64 on the same grid: fine
     // bin f of coarse bin k is 64 k + (63 - (floor(64 y) - 64 floor(y)))):
-    // by a lone block in the same pass; after a shared pass by the finisher,
-    // which visits only the runs of TP_RUN tokens the pass marked in the
-    // boundary area's bitmap (when it fits), else the whole row.
+    // by a lone block in the same pass; by a shared pass's blocks, when the
+    // range is at most TP_FINE_SHARED fine bins; else after a shared pass by
+    // the finisher, which visits only the runs of TP_RUN tokens the pass
+    // marked in the boundary area's bitmap (when it fits), else the whole row.
     const double fine_top = (top + 1) * FINE_PER_COARSE - 1;  // fine index of a token: fine_top - floor(y * 64)
     const double fine_base = double(b_lo) * FINE_PER_COARSE;
     const int nfine = (b_hi - b_lo + 1) * FINE_PER_COARSE;
@@ -2134,7 +2142,10 @@ template <int DT, bool VEC> struct FullRow {
     const int bitmap_words = int(min<int64_t>(bound_bitmap_words(a.vocab), INT_MAX));
     const bool marks = dense && shared_pass && bitmap_words <= bound_capacity(bin_slices);
     const bool fine_local = dense && !shared_pass;
-    if (fine_local) {
+    // A shared pass over a narrow dense range also bins it finer: each block
+    // its share in LDS, added to the row's fine bins before the arrival.
+    const bool fine_shared = marks && nfine <= TP_FINE_SHARED && bound_fine_fits(bin_slices, a.vocab);
+    if (fine_local || fine_shared) {
       for (int i = tid; i < nfine; i += BLOCK) { b.mass[i] = 0; b.cnt[i] = 0; }
       __syncthreads();
     }
@@ -2171,11 +2182,12 @@ template <int DT, bool VEC> struct FullRow {
                 const int slot = atomicAdd(&b.n, 1);
                 if (slot < GATHER_CAP) keys[slot] = gkey(v[j], t);
               }
-            } else if (marks) {
-              const int run = t / TP_RUN;
-              atomicOr(&gids[run >> 5], 1u << (run & 31));
-            } else if (fine_local) {
-              add_fine(v[j]);
+            } else {
+              if (marks) {
+                const int run = t / TP_RUN;
+                atomicOr(&gids[run >> 5], 1u << (run & 31));
+              }
+              if (fine_local || fine_shared) add_fine(v[j]);
             }
           }
         }
@@ -2191,6 +2203,17 @@ template <int DT, bool VEC> struct FullRow {
       queue_pass(g_begin, g_end, lowest, dp, sub, classify);
     }
     Pick best = dp.best;
+    if (fine_shared) {
+      __syncthreads();
+      double* const fm = bound_fine_mass(a, row, bin_slices);
+      uint32_t* const fc = bound_fine_count(a, row, bin_slices);
+      for (int i = tid; i < nfine; i += BLOCK) {
+        if (b.cnt[i]) {
+          atomicAdd(&fm[i], b.mass[i]);
+          atomicAdd(&fc[i], b.cnt[i]);
+        }
+      }
+    }
     if (shared_pass) {
       const Pick mine = block_pick(best, sh);
       if (tid == 0) {
@@ -2248,7 +2271,13 @@ template <int DT, bool VEC> struct FullRow {
       auto pick_of = [](const W (&x)[4], int j) { return j == 0 ? x[0] : j == 1 ? x[1] : j == 2 ? x[2] : x[3]; };
       // The marked runs, listed once for both passes (-1: the whole row).
       const int listed = marks ? list_runs(gids, bitmap_words) : -1;
-      if (!fine_local) {
+      if (fine_shared) {
+        // Every block's share, summed before the arrival.
+        const double* const fm = bound_fine_mass(a, row, bin_slices);
+        const uint32_t* const fc = bound_fine_count(a, row, bin_slices);
+        for (int i = tid; i < nfine; i += BLOCK) { b.mass[i] = fm[i]; b.cnt[i] = fc[i]; }
+        __syncthreads();
+      } else if (!fine_local) {
         // The finisher bins the coarse range finer: only the marked runs, or
         // the whole row when the bitmap did not fit or marks too many.
         for (int i = tid; i < nfine; i += BLOCK) { b.mass[i] = 0; b.cnt[i] = 0; }
@@ -3655,7 +3684,7 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(5)))
     // A binned top-p row: the slice's bins (n_cand TP_COARSE marks them
     // usable), its top bin in `frontier`, its reference maximum in `tau`.
     // The first slice readies the finishing blocks' arrival counter, gathered
-    // count and, when it fits the boundary area, the bitmap.
+    // count and, when they fit the boundary area, the bitmap and fine bins.
     if (slice == 0) {
       if (tid == 0) {
         counters(a, row)->bound = 0;
@@ -3665,6 +3694,11 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(5)))
       if (words <= bound_capacity(pl.slices)) {
         uint32_t* bitmap = bound_ids(a, row, pl.slices);
         for (int i = tid; i < int(words); i += BLOCK) bitmap[i] = 0;
+      }
+      if (bound_fine_fits(pl.slices, a.vocab)) {
+        double* fm = bound_fine_mass(a, row, pl.slices);
+        uint32_t* fc = bound_fine_count(a, row, pl.slices);
+        for (int i = tid; i < TP_FINE_SHARED; i += BLOCK) { fm[i] = 0; fc[i] = 0; }
       }
     }
     SliceBins sb;

@@ -116,6 +116,14 @@ constexpr int bound_capacity(int slices) {
 }
 // Bitmap words of a vocabulary.
 constexpr int64_t bound_bitmap_words(int64_t vocab) { return (vocab + 32 * TP_RUN - 1) / (32 * TP_RUN); }
+// After the bitmap (at an even word, so 8-byte aligned) and when it fits,
+// the fine bins of a dense range that the finishing blocks sum during their
+// pass: TP_FINE_SHARED FP64 masses, then as many 32-bit counts.
+constexpr int TP_FINE_SHARED = 128;
+constexpr int64_t bound_fine_offset(int64_t vocab) { return (bound_bitmap_words(vocab) + 1) & ~int64_t(1); }
+constexpr bool bound_fine_fits(int slices, int64_t vocab) {
+  return bound_fine_offset(vocab) + 3 * TP_FINE_SHARED <= bound_capacity(slices);
+}
 static_assert(bound_capacity(TP_SLICES_MAX) >= 960, "the boundary area holds 960 IDs at the most slices");
 static_assert(bound_bitmap_words(int64_t(TP_SLICES_MAX) * 16 * 4 * 256) <= bound_capacity(TP_SLICES_MAX),
               "the bitmap of the largest binned row fits the boundary area");
