@@ -1892,23 +1892,30 @@ template <int DT, bool VEC> struct FullRow {
     }
   }
 
-  // One pass over groups [g_begin, g_end), PQ_ROUND groups in flight per
-  // thread: a group holding a valid token with x32 >= lowest is queued on
-  // dp (those tokens' bits), and classify(g, queued, xs) settles the queued
-  // tokens as dp draws them (see DensePick::drain). Every thread calls it.
-  template <class C>
-  __device__ __forceinline__ void queue_pass(int g_begin, int g_end, float lowest, DensePick& dp, uint32_t sub,
-                                             C&& classify) {
+  // One pass over the groups group_at(i), i in [i_begin, i_end), PQ_ROUND
+  // groups in flight per thread: a group holding a valid token with lowest
+  // <= x32 <= highest is queued on dp (those tokens' bits), and
+  // classify(g, queued, xs) settles the queued tokens as dp draws them (see
+  // DensePick::drain). Every thread calls it.
+  struct SameGroup {
+    __device__ __forceinline__ int operator()(int i) const { return i; }
+  };
+  template <class C, class At = SameGroup>
+  __device__ __forceinline__ void queue_pass(int i_begin, int i_end, float lowest, DensePick& dp, uint32_t sub,
+                                             C&& classify, float highest = INFINITY, At group_at = At{}) {
     PickQueue& q = tb->pq;
-    for (int base0 = g_begin; base0 < g_end; base0 += BLOCK * PQ_ROUND) {  // a uniform trip count: dp's queue is per wave
+    for (int base0 = i_begin; base0 < i_end; base0 += BLOCK * PQ_ROUND) {  // a uniform trip count: dp's queue is per wave
       const int base = base0 + int(threadIdx.x);
       W x[PQ_ROUND][4];
       uint32_t bits[PQ_ROUND];
+      int gs[PQ_ROUND];
 #pragma unroll
       for (int u = 0; u < PQ_ROUND; ++u) {
-        const int g = base + u * BLOCK;
-        view.load(min(g, g_end - 1), x[u]);
-        bits[u] = g < g_end ? group_bits(a, row, g) : 0u;
+        const int i = base + u * BLOCK;
+        const int g = group_at(min(i, i_end - 1));
+        gs[u] = g;
+        view.load(min(g, groups - 1), x[u]);
+        bits[u] = i < i_end && g < groups ? group_bits(a, row, g) : 0u;
       }
 #pragma unroll
       for (int u = 0; u < PQ_ROUND; ++u) {
@@ -1916,9 +1923,10 @@ template <int DT, bool VEC> struct FullRow {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const W v = x[u][j];
-          if (((bits[u] >> j) & 1u) && v > neg_inf<W>() && tp.x32(v) >= lowest) queued |= 1u << j;
+          const float xv = tp.x32(v);
+          if (((bits[u] >> j) & 1u) && v > neg_inf<W>() && xv >= lowest && xv <= highest) queued |= 1u << j;
         }
-        dp.offer(q, base + u * BLOCK, queued);
+        dp.offer(q, gs[u], queued);
       }
       dp.drain(q, p.rng, sub, false, classify);
     }
@@ -2357,31 +2365,41 @@ template <int DT, bool VEC> struct FullRow {
       if (fcount == 0 || fcount > GATHER_CAP) return false;
       f_lo += int(base);  // absolute fine indices from here on
       f_hi += int(base);
-      // The second dense pass, by this block alone: the tokens of fine bins
-      // [f_lo, f_hi] gathered, the coarse range's tokens before f_lo drawn
-      // (the tokens before the coarse range were drawn in the first pass).
-      auto settle_group = [&](int g, const W (&x)[4], uint32_t bits) {
-        uint32_t draw = 0;
-        for (uint32_t m = screened(x, bits); m; m &= m - 1) {
-          const int j = __ffs(m) - 1;
-          const W v = pick_of(x, j);
-          double k;
-          if (!in_coarse(v, tp.x32(v), &k)) continue;
-          const double f = fine_of(v);
-          const int t = 4 * g + j;
-          if (f < double(f_lo)) {
-            if (t != excluded) draw |= 1u << j;
-          } else if (f <= double(f_hi)) {
-            const int slot = atomicAdd(&b.n, 1);
-            if (slot < GATHER_CAP) keys[slot] = gkey(v, t);
+      // The second dense pass, by this block alone, over the listed runs'
+      // groups or the whole row: the tokens of fine bins [f_lo, f_hi]
+      // gathered, the coarse range's tokens before f_lo drawn (the tokens
+      // before the coarse range were drawn in the first pass), queued and
+      // drawn densely as in the shared pass.
+      {
+        auto settle_queued = [&](int g, uint32_t queued, float (&xs)[4]) -> uint32_t {
+          W v[4];
+          view.load(g, v);
+          uint32_t draw = 0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            xs[j] = tp.x32(v[j]);
+            double k;
+            if (!((queued >> j) & 1u) || !in_coarse(v[j], xs[j], &k)) continue;
+            const double f = fine_of(v[j]);
+            const int t = 4 * g + j;
+            if (f < double(f_lo)) {
+              if (t != excluded) draw |= 1u << j;
+            } else if (f <= double(f_hi)) {
+              const int slot = atomicAdd(&b.n, 1);
+              if (slot < GATHER_CAP) keys[slot] = gkey(v[j], t);
+            }
           }
+          return draw;
+        };
+        if (listed >= 0) {
+          const uint32_t* list = run_list();
+          constexpr int GPR = TP_RUN / 4;  // groups per run
+          auto listed_group = [list](int i) { return int(list[i / GPR]) * GPR + i % GPR; };
+          queue_pass(0, listed * GPR, edge_range - SCREEN, dp, sub, settle_queued, edge_before + SCREEN, listed_group);
+        } else {
+          queue_pass(0, groups, edge_range - SCREEN, dp, sub, settle_queued, edge_before + SCREEN);
         }
-        if (draw)
-          pick_group<false, false>(g, x, draw, tp, p.rng, sub, -1, [](W, float) { return true; }, dp.best, dp.bar,
-                                   nullptr);
-      };
-      if (listed >= 0) listed_pass(listed, settle_group);
-      else each_group(settle_group);
+      }
       best = dp.best;
     }
     __syncthreads();
