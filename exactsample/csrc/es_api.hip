@@ -153,7 +153,7 @@ int32_t launch_call(const es_arguments& a, void* stream_ptr, bool own_workspace)
   pl.cap_slice = cap_total / pl.slices;
   pl.slice_blocks = int(a.rows * pl.slices);
   // A binned top-p row (list rows only) has its boundary pass shared by
-  // `parts` finishing blocks, each taking whole slices; the blocks of other
+  // `parts` finishing blocks, each taking an equal share of its groups; the blocks of other
   // rows exit at once. About one round of the device's resident finishing
   // blocks (two per CU) for the call, at least two per row.
   pl.helpers = 0;

@@ -4018,7 +4018,7 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments, Plan) {
         full.bin_slices = usable ? pl.slices : 0;
         full.parts = usable && pl.helpers > 0 ? pl.helpers + 1 : 1;
         full.part = part;
-        full.gps = pl.gps * ((pl.slices + pl.helpers) / (pl.helpers + 1));  // whole slices per block
+        full.gps = ((pl.groups + pl.helpers) / (pl.helpers + 1) + 1) & ~1;  // an even share: runs stay whole
       }
       if (part > 0 && full.parts == 1) return;  // only a shared boundary pass has helpers
       result = full.run(maximum, greedy, runner_up_id, valid);
