@@ -16,11 +16,11 @@
 //  writes a SlicePart with plain stores; the row's first slice also records
 //  the row's resolved request parameters and checks its per-row metadata.
 //
-//  es_finish, one block per row, then ceil(R / 256) request blocks that
-//  validate each request's metadata and write the outputs of every request
-//  that fails it (reference: csrc/verify/verify.cu:6-56, initialize), then
-//  Plan::helpers blocks per row that share a binned top-p row's boundary pass
-//  (and leave at once on other rows). A row block (the kernel boundary makes
+//  es_finish, one block per row, then Plan::helpers blocks per row that share
+//  a binned top-p row's boundary pass (and leave at once on other rows), then
+//  ceil(R / 256) request blocks that validate each request's metadata and
+//  write the outputs of every request that fails it (reference:
+//  csrc/verify/verify.cu:6-56, initialize). A row block (the kernel boundary makes
 //  every slice's stores visible) merges the slices in slice order and
 //  finishes the row:
 //    - failed and greedy rows directly;
@@ -3827,14 +3827,16 @@ __global__ void __launch_bounds__(BLOCK) es_finish(es_arguments, Plan) {
   __shared__ TopPBins tbins;  // the full-row path's binned top-p boundary
   const es_arguments& a = kernel_args().a;
   const Plan pl = kernel_args().pl;
-  // Blocks: one per row (part 0), the request blocks, then pl.helpers per row
-  // (parts 1 ... pl.helpers), which take part only in the boundary pass of a
-  // binned top-p row and otherwise leave at once.
-  const int64_t hb = int64_t(blockIdx.x) - a.rows - pl.req_blocks;
-  if (int64_t(blockIdx.x) >= a.rows && hb < 0) {
-    request_block(a, int(int64_t(blockIdx.x) - a.rows));
+  // Blocks: one per row (part 0), then pl.helpers per row (parts 1 ...
+  // pl.helpers), which take part only in the boundary pass of a binned top-p
+  // row and otherwise leave at once, then the request blocks. The request
+  // blocks wait on nothing, so the rows' blocks take the device's first slots.
+  const int64_t n_helpers = a.rows * pl.helpers;
+  if (int64_t(blockIdx.x) >= a.rows + n_helpers) {
+    request_block(a, int(int64_t(blockIdx.x) - a.rows - n_helpers));
     return;
   }
+  const int64_t hb = int64_t(blockIdx.x) - a.rows;  // >= 0: a helper block
   const int64_t row = hb >= 0 ? hb / pl.helpers : int64_t(blockIdx.x);
   const int part = hb >= 0 ? 1 + int(hb - row * pl.helpers) : 0;
   const int tid = threadIdx.x;

@@ -14,7 +14,7 @@ struct Plan {
   int32_t slices;        // blocks per row
   int32_t groups;        // groups of 4 tokens per row
   int32_t gps;           // groups per slice
-  int32_t req_blocks;    // request blocks, after the row blocks of es_finish
+  int32_t req_blocks;    // request blocks, last in es_finish's grid
   int32_t cap_slice;     // candidates one slice may store
   int32_t slice_blocks;  // rows x slices: es_main's grid
   int32_t tiles;         // register tiles per slice (> 1 only for vocabularies past MAX_SLICES tiles)
