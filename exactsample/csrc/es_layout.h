@@ -124,6 +124,7 @@ constexpr int64_t bound_fine_offset(int64_t vocab) { return (bound_bitmap_words(
 constexpr bool bound_fine_fits(int slices, int64_t vocab) {
   return bound_fine_offset(vocab) + 3 * TP_FINE_SHARED <= bound_capacity(slices);
 }
+static_assert(bound_fine_fits(TP_SLICES_MAX, 151936), "the shared fine bins fit a 151,936-token row at the most slices");
 static_assert(bound_capacity(TP_SLICES_MAX) >= 960, "the boundary area holds 960 IDs at the most slices");
 static_assert(bound_bitmap_words(int64_t(TP_SLICES_MAX) * 16 * 4 * 256) <= bound_capacity(TP_SLICES_MAX),
               "the bitmap of the largest binned row fits the boundary area");
